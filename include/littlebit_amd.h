@@ -1,0 +1,109 @@
+/*
+ * littlebit_amd.h -- C ABI of the MI355X (gfx950) LittleBitLinear forward.
+ *
+ *   y = sum_b  h_b * (U_b_sign . (l_b * (V_b_sign^T . (g_b * x))))  [+ bias]
+ *
+ * per projection, with bit-packed +-1 latent factors (one bit per sign) and
+ * fp32 row / latent / column scales.  b runs over the draft ("main") branch
+ * and an optional residual branch whose rank may differ from the main one.
+ *
+ * Conventions
+ *   - Every pointer is device memory owned by the caller.  Nothing here
+ *     allocates device memory or synchronises the host.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL is the
+ *     null stream) and is ordered with the caller's other work on it.
+ *   - Sign words use the reference packing (LSB first, bit 1 == -1,
+ *     pad bits 0 == +1); pass int32 or uint32 words, only the bits matter.
+ *   - Return value 0 on success, a negative LBK_ERR_* code otherwise; the
+ *     message of the last failure on the calling thread is lbk_last_error().
+ *   - Stateless apart from the caller's workspace; calls on different streams
+ *     must use different workspaces.
+ */
+#ifndef LITTLEBIT_AMD_H
+#define LITTLEBIT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LBK_ABI_VERSION 1
+
+/* Element types of activations and outputs. */
+#define LBK_F32 0
+#define LBK_BF16 1
+
+/* Error codes. */
+#define LBK_OK 0
+#define LBK_ERR_ARG (-1)       /* bad shape, null pointer, unsupported size */
+#define LBK_ERR_DTYPE (-2)     /* unsupported element type */
+#define LBK_ERR_WORKSPACE (-3) /* workspace missing or too small */
+#define LBK_ERR_HIP (-4)       /* a HIP call or kernel launch failed */
+
+/* One LittleBit branch of a projection with in_features K, out_features N.
+ * Field names follow the runtime checkpoint keys of
+ * convert_hf_to_runtime.py:46-57 (v_sign_rt, mid, u_sign_rt, u1, v2). */
+typedef struct lbk_branch {
+  const int32_t* v_sign; /* [rank, ceil(K/32)]  sign(V), packed along K     */
+  const int32_t* u_sign; /* [N, ceil(rank/32)]  sign(U), packed along rank  */
+  const float* v2;       /* [K]     column scale g                          */
+  const float* mid;      /* [rank]  latent scale l = v1 * u2                */
+  const float* u1;       /* [N]     row scale h                             */
+  int64_t rank;          /* R >= 1                                          */
+} lbk_branch;
+
+/* ABI version (LBK_ABI_VERSION of the build). */
+int lbk_abi_version(void);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* lbk_last_error(void);
+
+/* Bytes of workspace lbk_linear_forward needs for these shapes.
+ * Returns 0 with the error set if the shapes are invalid. */
+size_t lbk_linear_workspace_bytes(const lbk_branch* branches, int n_branches,
+                                  int64_t M, int64_t K, int64_t N);
+
+/* Fused LittleBitLinear forward: every branch, the branch sum and the bias.
+ *   x: [M, K] of x_dtype (LBK_F32 | LBK_BF16), row-major, contiguous
+ *   y: [M, N] of y_dtype (LBK_F32 | LBK_BF16), row-major, contiguous
+ *   bias: [N] fp32 or NULL
+ *   n_branches: 1 (draft) or 2 (draft + residual)
+ * Replaces LittleBitLinear.forward / _compute_forward
+ * (quantization/modules/littlebit.py:95-121), whose GPU form is two dense
+ * matmuls on +-1 factors unpacked to the activation dtype. */
+int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M,
+                       int64_t K, int64_t N, const void* x, int x_dtype,
+                       const float* bias, void* y, int y_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* One-branch form with the argument list of the reference operator
+ * littlebit_cpu_ops::littlebit_linear (patches/littlebit_cpu_optimized.cpp:
+ * 598-701, schema at :2324-2329): input [M, v_cols] fp32, v2 [1, v_cols],
+ * v_sign [R, ceil(v_cols/32)], mid [1, R], u_sign [N, ceil(u_cols/32)],
+ * u1 [1, N], u_cols == R; output [M, N] fp32.  The reference quantises the
+ * activations to int8 at both stages; this computes in fp32 throughout. */
+int lbk_littlebit_linear(const float* input, int64_t M, const float* v2,
+                         const int32_t* v_sign, int64_t v_cols,
+                         const float* mid, const int32_t* u_sign,
+                         int64_t u_cols, const float* u1, int64_t out_features,
+                         float* output, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Expand packed signs to int8 {-1,+1}: out [rows, cols].
+ * Replaces binary_unpacker (quantization/utils/binary_packer.py:54-97). */
+int lbk_unpack_signs(const int32_t* packed, int64_t rows, int64_t cols,
+                     int8_t* out, void* stream);
+
+/* Pack int8 signs to words: out [rows, ceil(cols/32)]; s < 0 -> bit 1, else
+ * bit 0, pad bits 0.  Same words as binary_packer
+ * (quantization/utils/binary_packer.py:5-51) for inputs in {-1, +1}. */
+int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols,
+                   int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITTLEBIT_AMD_H */

@@ -1,0 +1,27 @@
+"""MI355X-native LittleBitLinear forward (HIP kernels for gfx950 behind a C ABI).
+
+Public surface:
+  * :class:`LittleBitLinear` -- drop-in for quantization/modules/littlebit.py
+  * :func:`littlebit_linear` -- GPU form of the reference operator
+    ``littlebit_cpu_ops::littlebit_linear``
+  * :class:`LittleBitProjection` / :class:`LittleBitBranch` -- prepared fused
+    forward of a projection's draft and residual branches
+  * :func:`binary_packer` / :func:`binary_unpacker` -- the reference word format
+"""
+from .binary_packer import binary_packer, binary_unpacker, words_per_row
+from .ops import LittleBitBranch, LittleBitProjection, littlebit_forward, littlebit_linear
+from .modules import LittleBitLinear, sign_pm1
+
+__all__ = [
+    "LittleBitLinear",
+    "LittleBitBranch",
+    "LittleBitProjection",
+    "littlebit_forward",
+    "littlebit_linear",
+    "binary_packer",
+    "binary_unpacker",
+    "words_per_row",
+    "sign_pm1",
+]
+
+__version__ = "0.1.0"

@@ -1,0 +1,244 @@
+"""Operator-level entry points of the HIP LittleBitLinear forward.
+
+* :func:`littlebit_linear` keeps the schema and argument checks of the
+  reference operator ``littlebit_cpu_ops::littlebit_linear``
+  (patches/littlebit_cpu_optimized.cpp:2324-2329, checks at :607-634) but
+  runs on a GPU and computes in fp32 (the reference quantises activations to
+  int8 at both stages, patch:669 and :684).
+* :class:`LittleBitBranch` / :class:`LittleBitProjection` hold one
+  projection's device-resident packed factors and scales and run the fused
+  forward (all branches + bias in one call) through ``lbk_linear_forward``.
+
+Everything here requires CUDA (HIP) tensors; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "LittleBitBranch",
+    "LittleBitProjection",
+    "littlebit_linear",
+    "littlebit_forward",
+    "workspace_for",
+]
+
+_DTYPE_CODES = {torch.float32: _lib.LBK_F32, torch.bfloat16: _lib.LBK_BF16}
+
+# (device index, stream handle) -> uint8 workspace tensor
+_workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def workspace_for(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Per-(device, stream) scratch buffer, grown on demand and kept."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), int(stream))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    _check(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _check(t.is_cuda, f"{name} must be a GPU tensor (the HIP path has no CPU fallback)")
+    _check(t.is_contiguous(), f"{name} must be contiguous")
+
+
+@dataclass
+class LittleBitBranch:
+    """One branch's device tensors, in the runtime-checkpoint naming.
+
+    v_sign [R, ceil(K/32)] int32 (``v_sign_rt``), u_sign [N, ceil(R/32)] int32
+    (``u_sign_rt``), v2 [K] fp32, mid [R] fp32 (= v1*u2), u1 [N] fp32
+    (convert_hf_to_runtime.py:46-57).
+    """
+
+    v_sign: torch.Tensor
+    u_sign: torch.Tensor
+    v2: torch.Tensor
+    mid: torch.Tensor
+    u1: torch.Tensor
+
+    @property
+    def rank(self) -> int:
+        return int(self.v_sign.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.v2.numel())
+
+    @property
+    def out_features(self) -> int:
+        return int(self.u1.numel())
+
+    def validate(self, K: int, N: int, name: str = "branch") -> None:
+        R = self.rank
+        for t, nm in ((self.v_sign, "v_sign"), (self.u_sign, "u_sign"), (self.v2, "v2"),
+                      (self.mid, "mid"), (self.u1, "u1")):
+            _require_cuda(t, f"{name}.{nm}")
+        _check(self.v_sign.dtype == torch.int32, f"{name}.v_sign must be int32")
+        _check(self.u_sign.dtype == torch.int32, f"{name}.u_sign must be int32")
+        for t, nm in ((self.v2, "v2"), (self.mid, "mid"), (self.u1, "u1")):
+            _check(t.dtype == torch.float32, f"{name}.{nm} must be float32")
+        _check(self.v_sign.dim() == 2 and self.v_sign.shape[1] == (K + 31) // 32,
+               f"{name}.v_sign must have shape [R, ceil(K/32)] = [{R}, {(K + 31) // 32}], got {tuple(self.v_sign.shape)}")
+        _check(self.u_sign.dim() == 2 and tuple(self.u_sign.shape) == (N, (R + 31) // 32),
+               f"{name}.u_sign must have shape [N, ceil(R/32)] = [{N}, {(R + 31) // 32}], got {tuple(self.u_sign.shape)}")
+        _check(self.v2.numel() == K, f"{name}.v2 must have K={K} elements")
+        _check(self.mid.numel() == R, f"{name}.mid must have R={R} elements")
+        _check(self.u1.numel() == N, f"{name}.u1 must have N={N} elements")
+        dev = self.v_sign.device
+        for t in (self.u_sign, self.v2, self.mid, self.u1):
+            _check(t.device == dev, f"{name}: all tensors must be on one device")
+
+
+class LittleBitProjection:
+    """A projection's branches (draft, optional residual) and optional bias,
+    prepared once so that each forward is one C call."""
+
+    def __init__(self, branches: Sequence[LittleBitBranch], bias: Optional[torch.Tensor] = None):
+        _check(1 <= len(branches) <= 2, "a projection has one or two branches")
+        self.branches = list(branches)
+        self.in_features = self.branches[0].in_features
+        self.out_features = self.branches[0].out_features
+        for i, b in enumerate(self.branches):
+            b.validate(self.in_features, self.out_features, f"branch{i}")
+        self.device = self.branches[0].v_sign.device
+        if bias is not None:
+            _require_cuda(bias, "bias")
+            _check(bias.dtype == torch.float32 and bias.numel() == self.out_features,
+                   "bias must be float32 with out_features elements")
+            _check(bias.device == self.device, "bias must be on the factors' device")
+        self.bias = bias
+        arr = (_lib.LbkBranch * len(self.branches))()
+        for i, b in enumerate(self.branches):
+            arr[i].v_sign = b.v_sign.data_ptr()
+            arr[i].u_sign = b.u_sign.data_ptr()
+            arr[i].v2 = b.v2.data_ptr()
+            arr[i].mid = b.mid.data_ptr()
+            arr[i].u1 = b.u1.data_ptr()
+            arr[i].rank = b.rank
+        self._arr = arr
+
+    @property
+    def ranks(self) -> Tuple[int, ...]:
+        return tuple(b.rank for b in self.branches)
+
+    def workspace_bytes(self, M: int) -> int:
+        lib = _lib.load()
+        n = lib.lbk_linear_workspace_bytes(self._arr, len(self.branches), int(M), self.in_features,
+                                           self.out_features)
+        if n == 0 and M > 0:
+            _lib.check(_lib.LBK_ERR_ARG, "lbk_linear_workspace_bytes")
+        return int(n)
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """y[..., N] = sum of branches (+ bias) for x[..., K] (fp32 or bf16)."""
+        _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
+        _check(x.device == self.device, "input must be on the factors' device")
+        _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
+        _check(x.shape[-1] == self.in_features,
+               f"input last dimension {x.shape[-1]} != in_features {self.in_features}")
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        M = x2.shape[0]
+        odt = out_dtype or x.dtype
+        _check(odt in _DTYPE_CODES, f"output dtype {odt} unsupported")
+        if out is None:
+            out = torch.empty((*lead, self.out_features), dtype=odt, device=x.device)
+        else:
+            _check(out.is_cuda and out.is_contiguous() and out.dtype == odt
+                   and out.numel() == M * self.out_features, "out has the wrong shape, dtype or layout")
+        if M == 0:
+            return out
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        need = self.workspace_bytes(M)
+        ws = workspace_for(x.device, stream, need)
+        rc = lib.lbk_linear_forward(
+            self._arr, len(self.branches), M, self.in_features, self.out_features,
+            x2.data_ptr(), _DTYPE_CODES[x.dtype],
+            self.bias.data_ptr() if self.bias is not None else None,
+            out.data_ptr(), _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "lbk_linear_forward")
+        return out
+
+    __call__ = forward
+
+
+def littlebit_forward(x: torch.Tensor, branches: Sequence[LittleBitBranch],
+                      bias: Optional[torch.Tensor] = None,
+                      out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """One-shot fused forward (prepares a :class:`LittleBitProjection`)."""
+    return LittleBitProjection(branches, bias).forward(x, out_dtype=out_dtype)
+
+
+def littlebit_linear(input: torch.Tensor, v2: torch.Tensor, v_sign: torch.Tensor, v_cols: int,
+                     mid: torch.Tensor, u_sign: torch.Tensor, u_cols: int,
+                     u1: torch.Tensor) -> torch.Tensor:
+    """GPU counterpart of ``torch.ops.littlebit_cpu_ops.littlebit_linear``.
+
+    Same arguments and the same precondition checks (patch:607-634, raised as
+    RuntimeError), output fp32 [M, N]; computed in fp32 without the
+    reference's int8 activation quantisation.
+    """
+    for t, nm in ((input, "input"), (v2, "v2"), (mid, "mid"), (u1, "u1")):
+        _require_cuda(t, nm)
+        _check(t.dtype == torch.float32, f"{nm} must be float32")
+    for t, nm in ((v_sign, "v_sign"), (u_sign, "u_sign")):
+        _require_cuda(t, nm)
+        _check(t.dtype == torch.int32, f"{nm} must be int32")
+    _check(input.dim() == 2, "input must have shape [M, K]")
+    _check(v2.dim() == 2 and v2.size(0) == 1, "v2 must have shape [1, K]")
+    _check(mid.dim() == 2 and mid.size(0) == 1, "mid must have shape [1, R]")
+    _check(u1.dim() == 2 and u1.size(0) == 1, "u1 must have shape [1, N]")
+    _check(input.size(1) == v_cols, "input K must match v_cols")
+    _check(v2.size(1) == v_cols, "v2 second dimension must match v_cols")
+    _check(v_sign.dim() == 2, "v_sign must have shape [R, ceil(K/32)]")
+    _check(u_sign.dim() == 2, "u_sign must have shape [N, ceil(R/32)]")
+    _check(v_sign.size(0) == mid.size(1), "mid rank must match v_sign rows")
+    _check(u_sign.size(0) == u1.size(1), "u1 out_features must match u_sign rows")
+    _check(mid.size(1) == u_cols, "mid rank must match u_cols")
+    _check(v_sign.size(1) == (v_cols + 31) // 32, "v_sign second dimension must equal ceil(v_cols / 32)")
+    _check(u_sign.size(1) == (u_cols + 31) // 32, "u_sign second dimension must equal ceil(u_cols / 32)")
+    dev = input.device
+    for t in (v2, v_sign, mid, u_sign, u1):
+        _check(t.device == dev, "all tensors must be on one device")
+    M = input.size(0)
+    N = u_sign.size(0)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    if M == 0:
+        return out
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    br = (_lib.LbkBranch * 1)()
+    br[0].v_sign = v_sign.data_ptr()
+    br[0].u_sign = u_sign.data_ptr()
+    br[0].v2 = v2.data_ptr()
+    br[0].mid = mid.data_ptr()
+    br[0].u1 = u1.data_ptr()
+    br[0].rank = int(u_cols)
+    need = lib.lbk_linear_workspace_bytes(br, 1, M, int(v_cols), N)
+    if need == 0:
+        _lib.check(_lib.LBK_ERR_ARG, "littlebit_linear")
+    ws = workspace_for(dev, stream, int(need))
+    rc = lib.lbk_littlebit_linear(input.data_ptr(), M, v2.data_ptr(), v_sign.data_ptr(), int(v_cols),
+                                  mid.data_ptr(), u_sign.data_ptr(), int(u_cols), u1.data_ptr(), N,
+                                  out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "littlebit_linear")
+    return out

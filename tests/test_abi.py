@@ -1,0 +1,118 @@
+"""The C ABI: the built library loads and exports every function that
+include/*.h declares, with the binding's argument lists in step.  No GPU work
+is issued: the error paths checked here return before any HIP call."""
+import ctypes
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(lbk_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert {"lbk_linear_forward", "lbk_littlebit_linear", "lbk_unpack_signs", "lbk_pack_signs",
+            "lbk_abi_version", "lbk_last_error", "lbk_linear_workspace_bytes"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+
+
+def test_binding_covers_header_exactly():
+    import littlebit_amd._lib as L
+    assert set(L.SIGNATURES) == declared_functions()
+
+
+def test_abi_version_matches_header():
+    import littlebit_amd._lib as L
+    text = (ROOT / "include" / "littlebit_amd.h").read_text()
+    ver = int(re.search(r"#define LBK_ABI_VERSION (\d+)", text).group(1))
+    assert L.load().lbk_abi_version() == ver
+
+
+def test_constants_match_header():
+    import littlebit_amd._lib as L
+    text = (ROOT / "include" / "littlebit_amd.h").read_text()
+    for name in ("LBK_F32", "LBK_BF16", "LBK_OK"):
+        assert int(re.search(rf"#define {name} (\d+)", text).group(1)) == getattr(L, name)
+    for name in ("LBK_ERR_ARG", "LBK_ERR_DTYPE", "LBK_ERR_WORKSPACE", "LBK_ERR_HIP"):
+        assert int(re.search(rf"#define {name} \((-\d+)\)", text).group(1)) == getattr(L, name)
+
+
+def test_struct_layout():
+    import littlebit_amd._lib as L
+    assert ctypes.sizeof(L.LbkBranch) == 6 * 8
+    assert L.LbkBranch.rank.offset == 40
+
+
+def _branch(rank=8):
+    import littlebit_amd._lib as L
+    b = (L.LbkBranch * 2)()
+    for i in range(2):
+        b[i].v_sign = b[i].u_sign = b[i].v2 = b[i].mid = b[i].u1 = 0x1000
+        b[i].rank = rank
+    return b
+
+
+def test_validation_errors_without_gpu_work():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    br = _branch()
+    fwd = lib.lbk_linear_forward
+    # bad branch count
+    assert fwd(br, 3, 1, 64, 64, 0x1000, L.LBK_F32, None, 0x1000, L.LBK_F32, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert "n_branches" in L.last_error()
+    # bad K
+    assert fwd(br, 1, 1, 0, 64, 0x1000, L.LBK_F32, None, 0x1000, L.LBK_F32, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    # bad dtype
+    assert fwd(br, 1, 1, 64, 64, 0x1000, 7, None, 0x1000, L.LBK_F32, 0x1000, 1 << 20, None) == L.LBK_ERR_DTYPE
+    # workspace too small
+    assert fwd(br, 2, 4, 64, 64, 0x1000, L.LBK_F32, None, 0x1000, L.LBK_F32, 0x1000, 16, None) == L.LBK_ERR_WORKSPACE
+    assert "workspace" in L.last_error()
+    # null factor pointer
+    br[0].u_sign = 0
+    assert fwd(br, 1, 1, 64, 64, 0x1000, L.LBK_F32, None, 0x1000, L.LBK_F32, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    # M == 0 is a no-op success
+    br[0].u_sign = 0x1000
+    assert fwd(br, 1, 0, 64, 64, None, L.LBK_F32, None, None, L.LBK_F32, None, 0, None) == L.LBK_OK
+
+
+def test_workspace_query():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    br = _branch(rank=100)
+    n1 = lib.lbk_linear_workspace_bytes(br, 1, 8, 4096, 4096)
+    n2 = lib.lbk_linear_workspace_bytes(br, 2, 8, 4096, 4096)
+    assert n1 > 0 and n2 > n1
+    assert lib.lbk_linear_workspace_bytes(br, 5, 8, 4096, 4096) == 0
+
+
+def test_pack_unpack_argument_errors():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    assert lib.lbk_unpack_signs(None, -1, 4, None, None) == L.LBK_ERR_ARG
+    assert lib.lbk_pack_signs(None, 2, -4, None, None) == L.LBK_ERR_ARG
+    assert lib.lbk_unpack_signs(None, 0, 4, None, None) == L.LBK_OK  # empty: nothing to do
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    import littlebit_amd._lib as L
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setattr(L, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(L.LittleBitLibraryMissing):
+        L.load()

@@ -1,0 +1,247 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bar: sign unpacking bit-exact; forward
+max|y - y_ref| / max|y_ref| <= 1e-3 for fp32 outputs.  bf16 outputs add the
+rounding of the output itself (relative 2**-9 per element), so their bar is
+4e-3.  Inputs are the seeded generator's (numpy PCG64).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import littlebit_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16_OUT = 4e-3
+
+
+def _dev_branch(b, dev):
+    from littlebit_amd import LittleBitBranch
+    return LittleBitBranch(
+        v_sign=torch.from_numpy(np.ascontiguousarray(b["v_sign"])).to(dev),
+        u_sign=torch.from_numpy(np.ascontiguousarray(b["u_sign"])).to(dev),
+        v2=torch.from_numpy(np.asarray(b["g"], np.float32)).to(dev),
+        mid=torch.from_numpy(np.asarray(b["l"], np.float32)).to(dev),
+        u1=torch.from_numpy(np.asarray(b["h"], np.float32)).to(dev),
+    )
+
+
+def _run(dev, x, branches, bias=None, x_dtype=torch.float32, out_dtype=None):
+    from littlebit_amd import LittleBitProjection
+    proj = LittleBitProjection([_dev_branch(b, dev) for b in branches],
+                               None if bias is None else torch.from_numpy(bias).to(dev))
+    tx = torch.from_numpy(np.asarray(x, np.float32)).to(dev).to(x_dtype)
+    y = proj.forward(tx, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), tx.float().cpu().numpy()
+
+
+def _synthetic(seed, M, K, N, ranks):
+    from littlebit_amd.synthetic import make_projection
+    x, brs = make_projection(seed, M, K, N, ranks)
+    return x, [b.as_dict() for b in brs]
+
+
+def _check(y, x_used, branches, K, N, tol, bias=None, what=""):
+    ref = O.littlebit_forward(x_used, branches, K, N, bias=bias)
+    err = O.rel_err(y, ref)
+    print(f"[parity] {what} rel_err={err:.3e}", flush=True)
+    assert err <= tol, f"{what}: rel_err {err:.3e} > {tol}"
+    return err
+
+
+# --------------------------------------------------------------------------- sign unpack / pack
+@pytest.mark.parametrize("rows,cols", [(1, 32), (5, 70), (205, 4096), (4096, 205), (7, 1843)])
+def test_unpack_bit_exact(gpu, rows, cols):
+    from littlebit_amd import binary_unpacker
+    rng = np.random.Generator(np.random.PCG64(rows * 7919 + cols))
+    wpr = (cols + 31) // 32
+    words = rng.integers(0, 2**32, size=(rows, wpr), dtype=np.uint64).astype(np.uint32)
+    words[0, 0] = 0x80000000  # bit 31 only
+    if rows > 1:
+        words[1, -1] = 0xFFFFFFFF  # pad bits set: must be ignored
+    w32 = words.view(np.int32)
+    out = binary_unpacker(torch.from_numpy(w32).to(gpu), (rows, cols)).cpu().numpy()
+    assert (out == O.unpack_signs(w32, (rows, cols))).all()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (5, 70), (205, 4096), (11008, 298)])
+def test_pack_bit_exact(gpu, rows, cols):
+    from littlebit_amd import binary_packer
+    rng = np.random.Generator(np.random.PCG64(rows + 31 * cols))
+    s = (1 - 2 * rng.integers(0, 2, size=(rows, cols))).astype(np.int8)
+    out = binary_packer(torch.from_numpy(s).to(gpu)).cpu().numpy()
+    assert (out == O.pack_signs(s)).all()
+
+
+# --------------------------------------------------------------------------- forward
+def test_golden_fixtures(gpu, forward_cases):
+    for c in forward_cases:
+        y, _ = _run(gpu, c["x"], c["branches"], bias=c["bias"])
+        err = O.rel_err(y, c["y"])
+        print(f"[parity] fixture {c['name']} rel_err={err:.3e}", flush=True)
+        assert err <= 1e-5, c["name"]
+
+
+def test_config0_gemv(gpu):
+    K = N = 4096
+    x, brs = _synthetic(1000, 1, K, N, [205])
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what="config0 M=1")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_config1_draft_plus_residual(gpu, M):
+    K = N = 4096
+    x, brs = _synthetic(1001, M, K, N, [205, 1843])
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=f"config1 M={M}")
+
+
+@pytest.mark.parametrize("name,K,N,ranks,M", [
+    ("gate_up_verify", 4096, 11008, [298, 2686], 8),
+    ("down_verify", 11008, 4096, [298, 2686], 8),
+    ("down_draft", 11008, 4096, [298], 1),
+    ("qkv_tree32", 4096, 4096, [205, 1843], 32),
+])
+def test_llama_shapes(gpu, name, K, N, ranks, M):
+    x, brs = _synthetic(1003, M, K, N, ranks)
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=name)
+
+
+@pytest.mark.parametrize("M,K,N,ranks", [(3, 70, 45, [37]), (5, 33, 31, [31, 1]), (9, 1000, 77, [64, 95]),
+                                         (17, 96, 130, [3])])
+def test_ragged_shapes(gpu, M, K, N, ranks):
+    x, brs = _synthetic(77 + M, M, K, N, ranks)
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=f"ragged M={M} K={K} N={N} R={ranks}")
+
+
+def test_bias(gpu):
+    K, N = 300, 200
+    x, brs = _synthetic(5, 4, K, N, [40, 70])
+    bias = np.random.Generator(np.random.PCG64(5)).standard_normal(N).astype(np.float32)
+    y, xu = _run(gpu, x, brs, bias=bias)
+    _check(y, xu, brs, K, N, TOL_F32, bias=bias, what="bias")
+
+
+def test_bf16_in_fp32_out(gpu):
+    K = N = 4096
+    x, brs = _synthetic(1004, 8, K, N, [205, 1843])
+    y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.float32)
+    _check(y, xu, brs, K, N, TOL_F32, what="bf16 in / fp32 out")
+
+
+def test_bf16_in_bf16_out(gpu):
+    K = N = 4096
+    x, brs = _synthetic(1005, 64, K, N, [204, 1843])
+    y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.bfloat16)
+    _check(y, xu, brs, K, N, TOL_BF16_OUT, what="bf16 in / bf16 out M=64")
+
+
+def test_prefill_shape_small(gpu):
+    K, N = 4096, 4096
+    x, brs = _synthetic(1006, 256, K, N, [204, 1843])
+    y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.float32)
+    _check(y, xu, brs, K, N, TOL_F32, what="M=256")
+
+
+def test_empty_batch(gpu):
+    from littlebit_amd import LittleBitProjection
+    _, brs = _synthetic(3, 1, 64, 48, [8])
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    y = proj.forward(torch.empty((0, 64), device=gpu))
+    assert tuple(y.shape) == (0, 48)
+
+
+def test_leading_dims_preserved(gpu):
+    from littlebit_amd import LittleBitProjection
+    K, N = 128, 96
+    x, brs = _synthetic(4, 6, K, N, [16])
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    y = proj.forward(torch.from_numpy(x).to(gpu).reshape(2, 3, K))
+    assert tuple(y.shape) == (2, 3, N)
+    _check(y.reshape(6, N).cpu().numpy(), x, brs, K, N, TOL_F32, what="leading dims")
+
+
+def test_deterministic(gpu):
+    K = N = 4096
+    x, brs = _synthetic(1007, 8, K, N, [205, 1843])
+    y1, _ = _run(gpu, x, brs)
+    y2, _ = _run(gpu, x, brs)
+    assert np.array_equal(y1, y2)
+
+
+def test_graph_replay_matches_eager(gpu):
+    from littlebit_amd import LittleBitProjection
+    K = N = 4096
+    x, brs = _synthetic(1008, 4, K, N, [205, 1843])
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    tx = torch.from_numpy(x).to(gpu)
+    eager = proj.forward(tx).clone()
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        proj.forward(tx, out=out)  # sizes the per-stream workspace before capture
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        proj.forward(tx, out=out)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        tx.mul_(1.0)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------------------- module / op boundary
+def test_module_forward_matches_oracle(gpu):
+    from littlebit_amd import LittleBitLinear
+    K, N = 4096, 4096
+    x, brs = _synthetic(1009, 8, K, N, [205, 1843])
+    branches = [{"u_packed": torch.from_numpy(b["u_sign"]), "v_packed": torch.from_numpy(b["v_sign"]),
+                 "u1": torch.from_numpy(b["h"]).reshape(1, N), "v2": torch.from_numpy(b["g"]).reshape(1, K),
+                 "mid": torch.from_numpy(b["l"]).reshape(1, -1)} for b in brs]
+    m = LittleBitLinear.from_packed(K, N, branches, device=gpu)
+    y = m(torch.from_numpy(x).to(gpu).reshape(2, 4, K))
+    assert tuple(y.shape) == (2, 4, N) and y.dtype == torch.float32
+    _check(y.reshape(8, N).cpu().numpy(), x, brs, K, N, TOL_F32, what="LittleBitLinear module")
+
+
+def test_op_littlebit_linear_matches_oracle(gpu):
+    from littlebit_amd import littlebit_linear
+    K, N, R = 4096, 4096, 205
+    x, brs = _synthetic(1010, 2, K, N, [R])
+    b = brs[0]
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    y = littlebit_linear(d(x), d(b["g"]).reshape(1, K), d(b["v_sign"]), K, d(b["l"]).reshape(1, R),
+                         d(b["u_sign"]), R, d(b["h"]).reshape(1, N))
+    _check(y.cpu().numpy(), x, brs, K, N, TOL_F32, what="littlebit_linear op")
+
+
+def test_op_precondition_errors(gpu):
+    from littlebit_amd import littlebit_linear
+    K, N, R = 64, 32, 8
+    x, brs = _synthetic(1011, 1, K, N, [R])
+    b = brs[0]
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    args = [d(x), d(b["g"]).reshape(1, K), d(b["v_sign"]), K, d(b["l"]).reshape(1, R), d(b["u_sign"]), R,
+            d(b["h"]).reshape(1, N)]
+    bad_k = list(args)
+    bad_k[3] = K + 1
+    with pytest.raises(RuntimeError, match="v_cols"):
+        littlebit_linear(*bad_k)
+    bad_dtype = list(args)
+    bad_dtype[2] = bad_dtype[2].to(torch.int64)
+    with pytest.raises(RuntimeError, match="int32"):
+        littlebit_linear(*bad_dtype)
+    cpu_in = list(args)
+    cpu_in[0] = cpu_in[0].cpu()
+    with pytest.raises(RuntimeError, match="GPU"):
+        littlebit_linear(*cpu_in)
