@@ -168,8 +168,17 @@ class LittleBitLinear(nn.Linear):
             mid = v1.to(torch.float32) * u2.to(torch.float32)
             setattr(self, "v1" + sfx, nn.Parameter(v1.detach().clone(), requires_grad=False))
             setattr(self, "u2" + sfx, nn.Parameter(u2.detach().clone(), requires_grad=False))
+        else:
+            # runtime layout: only the fused latent scale exists
+            for nm in ("v1" + sfx, "u2" + sfx):
+                if nm in self._parameters:
+                    del self._parameters[nm]
         if branch == "main":
+            # the rank comes from the tensors, as in quant_util.py:259-297
             self.split_dim = R
+            self._split_dim_final = torch.tensor(R)
+            self._eff_bit_actual = torch.tensor(
+                self._compute_eff_bits(self.in_features, self.out_features, R, self.residual))
         else:
             self.split_dim_R = R
         setattr(self, "u1" + sfx, nn.Parameter(u1.detach().clone(), requires_grad=False))
@@ -209,10 +218,6 @@ class LittleBitLinear(nn.Linear):
                     branch, state_dict[rt_u], state_dict[rt_v], state_dict[prefix + "u1" + rsfx],
                     state_dict[prefix + "v2" + rsfx], mid=state_dict[prefix + "mid" + rsfx],
                     rank=int(shape_v[0]) if shape_v is not None else None)
-                # the runtime layout keeps only the fused latent scale
-                for nm in ("v1" + sfx, "u2" + sfx):
-                    if nm in self._parameters:
-                        del self._parameters[nm]
                 consumed.update({rt_u, rt_v, rt_u + "_shape", rt_v + "_shape", prefix + "u1" + rsfx,
                                  prefix + "v2" + rsfx, prefix + "mid" + rsfx})
             elif prefix + "U" + sfx in state_dict and prefix + "V" + sfx in state_dict:

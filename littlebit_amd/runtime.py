@@ -1,0 +1,159 @@
+"""Runtime checkpoint layout and loader.
+
+The key mapping must stay identical to convert_hf_to_runtime.py so that a
+checkpoint converted by the reference loads here unchanged:
+
+  HF packed key (littlebit.py:315-318)   runtime key (convert_hf_to_runtime.py:46-84)
+  <p>.U_packed / U_shape                 <p>.u_sign_rt / u_sign_rt_shape
+  <p>.V_packed / V_shape                 <p>.v_sign_rt / v_sign_rt_shape
+  <p>.u1, <p>.v2                         <p>.u1, <p>.v2            (passed through)
+  <p>.v1, <p>.u2                         <p>.mid = v1.float()*u2.float()
+  ..._R variants                         u_sign_r_rt, v_sign_r_rt, u1_r, v2_r, mid_r
+  other keys                             passed through, except the LittleBit
+                                         buffers _eff_bit_target, _split_dim_final,
+                                         _eff_bit_actual, _binarized
+
+``load_runtime_checkpoint`` reads ``littlebit_runtime.safetensors`` and
+``littlebit_runtime_config.json`` (the files convert_hf_to_runtime.py:238-300
+writes; the reference runtime's own loader lives in the un-vendored
+lb_kernels package, cpu_draft_model.py:158-160) and
+``runtime_projections`` turns every projection into a GPU-resident
+:class:`~littlebit_amd.ops.LittleBitProjection` with the words left packed.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from typing import Dict, Optional, Tuple
+
+import torch
+
+__all__ = [
+    "convert_state_dict",
+    "build_runtime_config",
+    "build_dummy_config",
+    "load_runtime_checkpoint",
+    "runtime_prefixes",
+    "runtime_projections",
+]
+
+_SKIP_SUFFIXES = ("._eff_bit_target", "._split_dim_final", "._eff_bit_actual", "._binarized")
+
+
+def convert_state_dict(hf_state: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+    """HF packed LittleBit state dict -> runtime layout (key table above)."""
+    prefixes = set()
+    for key in hf_state:
+        for marker in (".U_packed", ".U_R_packed"):
+            if key.endswith(marker):
+                prefixes.add(key[: -len(marker)])
+    out: Dict[str, torch.Tensor] = {}
+    used = set()
+    branches = (("", "", "U", "V"), ("_R", "_r", "U_R", "V_R"))
+    for p in sorted(prefixes):
+        for hf_sfx, rt_sfx, u_name, v_name in branches:
+            if f"{p}.{u_name}_packed" not in hf_state:
+                continue
+            tag = "_r" if rt_sfx else ""
+            out[f"{p}.u_sign{tag}_rt"] = hf_state[f"{p}.{u_name}_packed"]
+            out[f"{p}.u_sign{tag}_rt_shape"] = hf_state[f"{p}.{u_name}_shape"]
+            out[f"{p}.v_sign{tag}_rt"] = hf_state[f"{p}.{v_name}_packed"]
+            out[f"{p}.v_sign{tag}_rt_shape"] = hf_state[f"{p}.{v_name}_shape"]
+            out[f"{p}.u1{rt_sfx}"] = hf_state[f"{p}.u1{hf_sfx}"]
+            out[f"{p}.v2{rt_sfx}"] = hf_state[f"{p}.v2{hf_sfx}"]
+            v1 = hf_state[f"{p}.v1{hf_sfx}"].to(torch.float32)
+            u2 = hf_state[f"{p}.u2{hf_sfx}"].to(torch.float32)
+            out[f"{p}.mid{rt_sfx}"] = (v1 * u2).contiguous()
+            used.update(f"{p}.{n}" for n in (f"{u_name}_packed", f"{u_name}_shape", f"{v_name}_packed",
+                                              f"{v_name}_shape", f"u1{hf_sfx}", f"u2{hf_sfx}",
+                                              f"v1{hf_sfx}", f"v2{hf_sfx}"))
+    for key, value in hf_state.items():
+        if key in used or key.endswith(_SKIP_SUFFIXES):
+            continue
+        out[key] = value
+    return out
+
+
+def build_runtime_config(hf_config: Dict, littlebit_config: Dict) -> Dict:
+    """littlebit_runtime_config.json contents (convert_hf_to_runtime.py:216-235)."""
+    return {
+        "format_version": 1,
+        "checkpoint_format": "runtime",
+        "sign_storage": "row_i1",
+        "runtime_layout": "cpu_row_i1",
+        "base_model_id": hf_config.get("_name_or_path"),
+        "model_type": hf_config.get("model_type", "llama"),
+        "torch_dtype": "bfloat16",
+        "quant_func": littlebit_config.get("quant_func", "STEBinary"),
+        "eff_bit": littlebit_config.get("eff_bit", 0.1),
+        "split_dim": littlebit_config.get("split_dim"),
+        "residual": littlebit_config.get("residual", False),
+    }
+
+
+def build_dummy_config(hf_config: Dict, littlebit_config: Dict) -> Dict:
+    """dummy_llama3_config.json contents (convert_hf_to_runtime.py:193-213)."""
+    return {
+        "name": hf_config.get("_name_or_path", "llama"),
+        "hidden_size": hf_config["hidden_size"],
+        "intermediate_size": hf_config["intermediate_size"],
+        "num_hidden_layers": hf_config["num_hidden_layers"],
+        "num_attention_heads": hf_config["num_attention_heads"],
+        "num_key_value_heads": hf_config.get("num_key_value_heads", hf_config["num_attention_heads"]),
+        "vocab_size": hf_config["vocab_size"],
+        "rms_norm_eps": hf_config.get("rms_norm_eps", 1e-6),
+        "include_lm_head": False,
+        "eff_bit": littlebit_config.get("eff_bit", 0.1),
+        "residual": littlebit_config.get("residual", False),
+    }
+
+
+def load_runtime_checkpoint(path, device: str = "cpu") -> Tuple[Dict[str, torch.Tensor], Optional[Dict]]:
+    """(state_dict, runtime_config) from a converted runtime directory."""
+    from safetensors.torch import load_file
+
+    path = Path(path)
+    state = load_file(str(path / "littlebit_runtime.safetensors"), device=str(device))
+    cfg_path = path / "littlebit_runtime_config.json"
+    cfg = json.loads(cfg_path.read_text()) if cfg_path.exists() else None
+    return state, cfg
+
+
+def runtime_prefixes(state: Dict[str, torch.Tensor]):
+    return sorted(k[: -len(".u_sign_rt")] for k in state if k.endswith(".u_sign_rt"))
+
+
+def runtime_projections(state: Dict[str, torch.Tensor], device, residual: Optional[bool] = None,
+                        bias_suffix: str = ".bias"):
+    """{prefix: LittleBitProjection} for every projection in a runtime state dict.
+
+    ``residual=None`` uses the residual branch wherever it exists; False
+    builds draft-only projections (the draft model of speculative decoding);
+    True requires it.
+    """
+    from .ops import LittleBitBranch, LittleBitProjection
+
+    dev = torch.device(device)
+    out = {}
+
+    def branch(p, tag, sfx):
+        return LittleBitBranch(
+            v_sign=state[f"{p}.v_sign{tag}_rt"].to(dev, torch.int32).contiguous(),
+            u_sign=state[f"{p}.u_sign{tag}_rt"].to(dev, torch.int32).contiguous(),
+            v2=state[f"{p}.v2{sfx}"].to(dev, torch.float32).reshape(-1).contiguous(),
+            mid=state[f"{p}.mid{sfx}"].to(dev, torch.float32).reshape(-1).contiguous(),
+            u1=state[f"{p}.u1{sfx}"].to(dev, torch.float32).reshape(-1).contiguous(),
+        )
+
+    for p in runtime_prefixes(state):
+        brs = [branch(p, "", "")]
+        has_r = f"{p}.u_sign_r_rt" in state
+        if residual is True and not has_r:
+            raise KeyError(f"{p}: residual branch requested but absent")
+        if has_r and residual is not False:
+            brs.append(branch(p, "_r", "_r"))
+        bias = state.get(p + bias_suffix)
+        if bias is not None:
+            bias = bias.to(dev, torch.float32).contiguous()
+        out[p] = LittleBitProjection(brs, bias)
+    return out

@@ -1,0 +1,173 @@
+"""Host-side logic of the drop-in LittleBitLinear (no GPU work): split-dim
+bookkeeping of quantization/modules/littlebit.py:50-93, packed state-dict
+format (:307-345), both checkpoint layouts, and the conversion invariants the
+reference test pins (test_cpu_draft.py:75-97)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from littlebit_amd import LittleBitLinear, binary_packer, binary_unpacker, sign_pm1
+from littlebit_amd.runtime import convert_state_dict
+from oracle import littlebit_oracle as O
+
+
+def _convert(in_f, out_f, **kw):
+    m = nn.Linear(in_f, out_f, bias=kw.pop("bias", False), device="meta")
+    m.__class__ = LittleBitLinear
+    m.__quant_convert__(False, None, **kw)
+    return m
+
+
+def test_split_dim_hand_values():
+    # 0.1 BPW, 4096x4096, no residual: (4096*4096*0.1 - 16*8192) / (8192 + 16) = 188.4...
+    f = LittleBitLinear._estimate_split_dim(4096, 4096, 0.1, False)
+    assert f == pytest.approx((4096 * 4096 * 0.1 - 16 * 8192) / 8208)
+    assert LittleBitLinear._finalize_split_dim(f, 1024, 8) == 184
+    # residual: (a*b*e - 32(a+b)) / (2(a+b+16))
+    fr = LittleBitLinear._estimate_split_dim(4096, 11008, 1.0, True)
+    assert fr == pytest.approx((4096 * 11008 - 32 * 15104) / (2 * 15120))
+    assert LittleBitLinear._estimate_split_dim(4096, 4096, None, False) is None
+    assert LittleBitLinear._finalize_split_dim(None, 1024, 8) == 1024
+    assert LittleBitLinear._finalize_split_dim(3.0, 1024, 8) == 8       # rounds to 0 -> min
+    assert LittleBitLinear._finalize_split_dim(-50.0, 1024, 8) == 8
+    eb = LittleBitLinear._compute_eff_bits(4096, 4096, 184, False)
+    assert eb == pytest.approx((184 * 8208 + 16 * 8192) / 4096 ** 2)
+    ebr = LittleBitLinear._compute_eff_bits(4096, 4096, 184, True)
+    assert ebr == pytest.approx((184 * 2 * 8208 + 32 * 8192) / 4096 ** 2)
+    assert LittleBitLinear._compute_eff_bits(0, 5, 8, False) == float("inf")
+
+
+def test_quant_convert_buffers_and_meta_params():
+    m = _convert(256, 128, eff_bit=1.0, residual=True, ratio_factor=0.5)
+    f = LittleBitLinear._estimate_split_dim(256, 128, 1.0, True) * 0.5
+    assert m.split_dim == LittleBitLinear._finalize_split_dim(f, 1024, 8)
+    assert int(m._split_dim_final) == m.split_dim
+    assert m.eff_bit_target == pytest.approx(1.0)
+    names = {n for n, _ in m.named_parameters()}
+    assert {"U", "V", "u1", "u2", "v1", "v2", "U_R", "V_R", "u1_R", "u2_R", "v1_R", "v2_R"} <= names
+    assert m.weight is None and m.U.is_meta
+    assert tuple(m.U.shape) == (128, m.split_dim) and tuple(m.V.shape) == (m.split_dim, 256)
+
+
+def _hf_packed_state(prefix, rng, K, N, ranks, dtype=torch.bfloat16):
+    sd = {}
+    for sfx, R in zip(("", "_R"), ranks):
+        U = (1 - 2 * rng.integers(0, 2, size=(N, R))).astype(np.int8)
+        V = (1 - 2 * rng.integers(0, 2, size=(R, K))).astype(np.int8)
+        sd[f"{prefix}U{sfx}_packed"] = torch.from_numpy(O.pack_signs(U))
+        sd[f"{prefix}U{sfx}_shape"] = torch.tensor([N, R])
+        sd[f"{prefix}V{sfx}_packed"] = torch.from_numpy(O.pack_signs(V))
+        sd[f"{prefix}V{sfx}_shape"] = torch.tensor([R, K])
+        for nm, n in (("u1", N), ("u2", R), ("v1", R), ("v2", K)):
+            sd[f"{prefix}{nm}{sfx}"] = torch.from_numpy(rng.standard_normal((1, n)).astype(np.float32)).to(dtype)
+    return sd
+
+
+def test_load_hf_packed_keeps_words_and_fuses_mid():
+    rng = np.random.Generator(np.random.PCG64(1))
+    K, N = 100, 70
+    sd = _hf_packed_state("", rng, K, N, [13, 29])
+    m = _convert(K, N, split_dim=8, residual=True)
+    m.load_state_dict(sd, strict=False)
+    assert m._binarized and m.split_dim == 13 and m.split_dim_R == 29
+    assert torch.equal(m.U_packed, sd["U_packed"]) and torch.equal(m.V_R_packed, sd["V_R_packed"])
+    # mid = v1 * u2 (test_cpu_draft.py:75-84, atol 1e-6)
+    assert torch.allclose(m.mid, sd["v1"].float() * sd["u2"].float(), atol=1e-6)
+    assert torch.allclose(m.mid_R, sd["v1_R"].float() * sd["u2_R"].float(), atol=1e-6)
+    # state_dict is the packed format again, words identical
+    out = m.state_dict()
+    for k in ("U_packed", "V_packed", "U_R_packed", "V_R_packed"):
+        assert torch.equal(out[k], sd[k]), k
+    assert out["V_shape"].tolist() == [13, K] and out["U_R_shape"].tolist() == [N, 29]
+    assert not any(k in out for k in ("U", "V", "mid"))
+
+
+def test_runtime_conversion_invariants():
+    """convert_state_dict keeps words identical and writes mid = v1*u2
+    (test_cpu_draft.py:57-97)."""
+    rng = np.random.Generator(np.random.PCG64(2))
+    K, N = 64, 48
+    hf = {}
+    for p in ("model.layers.0.self_attn.q_proj.", "model.layers.0.mlp.down_proj."):
+        hf.update(_hf_packed_state(p, rng, K, N, [9, 17]))
+    hf["model.norm.weight"] = torch.ones(K)
+    hf["model.layers.0.self_attn.q_proj._eff_bit_actual"] = torch.tensor(0.1)
+    rt = convert_state_dict(hf)
+    prefixes = sorted({k[:-len(".u_sign_rt")] for k in rt if k.endswith(".u_sign_rt")})
+    assert len(prefixes) == 2
+    for p in prefixes:
+        for key in ("u_sign_rt", "u_sign_rt_shape", "v_sign_rt", "v_sign_rt_shape", "u1", "mid", "v2"):
+            assert f"{p}.{key}" in rt
+        assert torch.equal(rt[f"{p}.u_sign_rt"], hf[f"{p}.U_packed"])
+        assert torch.equal(rt[f"{p}.v_sign_r_rt"], hf[f"{p}.V_R_packed"])
+        assert torch.allclose(rt[f"{p}.mid"], hf[f"{p}.v1"].float() * hf[f"{p}.u2"].float(), atol=1e-6)
+        assert rt[f"{p}.mid"].dtype == torch.float32
+    assert "model.norm.weight" in rt
+    assert not any(k.endswith("._eff_bit_actual") for k in rt)
+
+
+def test_load_runtime_layout():
+    rng = np.random.Generator(np.random.PCG64(3))
+    K, N = 90, 33
+    rt = convert_state_dict(_hf_packed_state("p.", rng, K, N, [11, 40]))
+    sd = {k[2:]: v for k, v in rt.items()}
+    m = _convert(K, N, split_dim=8, residual=True)
+    m.load_state_dict(sd, strict=False)
+    assert m._binarized and m.split_dim == 11 and m.split_dim_R == 40
+    assert torch.equal(m.mid, sd["mid"].reshape(1, -1))
+    assert "v1" not in dict(m.named_parameters())
+
+
+def test_load_dense_signs_packs_them():
+    rng = np.random.Generator(np.random.PCG64(4))
+    K, N, R = 40, 30, 12
+    U = torch.from_numpy(rng.standard_normal((N, R)).astype(np.float32))
+    V = torch.from_numpy(rng.standard_normal((R, K)).astype(np.float32))
+    V[0, 0] = 0.0  # sign(0) == +1
+    sd = {"U": U, "V": V, "u1": torch.ones(1, N), "u2": torch.ones(1, R), "v1": torch.ones(1, R),
+          "v2": torch.ones(1, K)}
+    m = _convert(K, N, split_dim=R)
+    m.load_state_dict(sd, strict=False)
+    assert torch.equal(m.U_packed, torch.from_numpy(O.pack_signs(O.sign_pm1(U.numpy()))))
+    assert torch.equal(m.V_packed, torch.from_numpy(O.pack_signs(O.sign_pm1(V.numpy()))))
+
+
+def test_host_packer_matches_oracle():
+    rng = np.random.Generator(np.random.PCG64(5))
+    for cols in (1, 32, 33, 70, 205):
+        s = (1 - 2 * rng.integers(0, 2, size=(4, cols))).astype(np.int8)
+        w = binary_packer(torch.from_numpy(s))
+        assert (w.numpy() == O.pack_signs(s)).all()
+        assert (binary_unpacker(w, s.shape).numpy() == s).all()
+    with pytest.raises(TypeError):
+        binary_packer(torch.ones(2, 3, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        binary_unpacker(torch.zeros(2, 2, dtype=torch.int32), (2, 70))
+
+
+def test_sign_pm1_zero():
+    assert sign_pm1(torch.tensor([-1.5, 0.0, -0.0, 2.0])).tolist() == [-1, 1, 1, 1]
+
+
+def test_forward_refuses_cpu_and_unbinarised():
+    m = _convert(32, 16, split_dim=8)
+    with pytest.raises(RuntimeError, match="packed"):
+        m(torch.zeros(1, 32))
+    rng = np.random.Generator(np.random.PCG64(6))
+    m.load_state_dict(_hf_packed_state("", rng, 32, 16, [8]), strict=False)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.zeros(1, 32))
+
+
+def test_from_packed_runtime_branches_has_no_meta_tensors():
+    rng = np.random.Generator(np.random.PCG64(7))
+    K, N = 64, 40
+    brs = []
+    for R in (205, 37):
+        brs.append({"u_packed": torch.from_numpy(O.pack_signs((1 - 2 * rng.integers(0, 2, (N, R))).astype(np.int8))),
+                    "v_packed": torch.from_numpy(O.pack_signs((1 - 2 * rng.integers(0, 2, (R, K))).astype(np.int8))),
+                    "u1": torch.ones(1, N), "v2": torch.ones(1, K), "mid": torch.ones(1, R)})
+    m = LittleBitLinear.from_packed(K, N, brs)
+    assert m.split_dim == 205 and m.split_dim_R == 37 and int(m._split_dim_final) == 205
+    assert not any(t.is_meta for t in list(m.parameters()) + list(m.buffers()))
