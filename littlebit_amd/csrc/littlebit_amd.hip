@@ -8,13 +8,27 @@
 // where sV and sU are +-1 read from words packed LSB first, bit 1 == -1
 // (quantization/utils/binary_packer.py:36-50).
 //
-// Two launches per projection, both branches in each:
-//   latent_kernel : one wavefront per latent row r of every branch; lanes
-//                   stride over the row's words, the wave reduces, lane 0
-//                   writes t[m, r] (already multiplied by l[r]) to workspace.
-//   expand_kernel : t of both branches staged in LDS; LPR lanes per output
-//                   row n split the row's words, reduce with lane shuffles and
-//                   write h0*acc0 + h1*acc1 + bias.
+// Two launches per projection, both branches in each.
+//
+// MFMA path (M <= 16):
+//   latent_mfma_kernel  grid = row-blocks (64 latent rows of one branch) x
+//                       k-chunks.  The block writes bf16 hi/lo halves of
+//                       g*x for its k-chunk to LDS (the MFMA A operand: rows
+//                       0-7 = hi of m 0-7, rows 8-15 = lo); each wave expands
+//                       its 16 rows' sign bytes into +-1 bf16 B operands in
+//                       registers and runs v_mfma_f32_16x16x32_bf16.  Partial
+//                       sums of the k-chunks go to workspace; the last block
+//                       of a row-block to arrive (a per-row-block counter that
+//                       it resets) adds them in fixed order, scales by l and
+//                       writes t.
+//   expand_mfma_kernel  grid = 64 output rows per block.  t of both branches
+//                       is staged in LDS as bf16 hi/lo; each wave expands the
+//                       U sign bytes of its 16 rows and accumulates both
+//                       branches, then writes h0*y0 + h1*y1 + bias.
+// General path (any M): latent_valu_kernel / expand_valu_kernel, fp32 VALU.
+//
+// Splitting fp32 activations into bf16 hi + lo keeps the product error near
+// 2^-17 relative: +-1 is exact in bf16 and the MFMA accumulates in fp32.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -39,10 +53,480 @@ int set_error(int code, const char* fmt, ...) {
 constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int64_t kMaxDim = int64_t(1) << 24;     // K, N, M limit
-constexpr int64_t kMaxRankTotal = 16384;          // sum of branch ranks
-constexpr int kLdsBudget = 64 * 1024;             // t staging in expand_kernel
+constexpr int64_t kMaxDim = int64_t(1) << 24;  // K, N, M limit
+constexpr int64_t kMaxRankTotal = 16384;       // sum of branch ranks
+constexpr int kValuLdsBudget = 64 * 1024;      // t staging in expand_valu_kernel
+constexpr int kMaxLds = 159 * 1024;            // gfx950: 160 KB per workgroup, 1 KB kept for static LDS
+constexpr int kRowBlock = 64;                  // latent rows per latent_mfma block
+constexpr int kMaxMfmaM = 16;                  // MFMA path handles M <= 16
+constexpr int kCounterSlots = 1024;            // counters at the workspace start
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(uint32_t);
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// element helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+__device__ __forceinline__ void store_out(float* y, size_t i, float v) { y[i] = v; }
+__device__ __forceinline__ void store_out(uint16_t* y, size_t i, float v) { y[i] = f32_to_bf16(v); }
+
+
+// 8 consecutive floats from a 16-byte aligned address.
+__device__ __forceinline__ void load8(const float* p, float (&a)[8]) {
+  const float4 u = *reinterpret_cast<const float4*>(p);
+  const float4 w = *reinterpret_cast<const float4*>(p + 4);
+  a[0] = u.x; a[1] = u.y; a[2] = u.z; a[3] = u.w;
+  a[4] = w.x; a[5] = w.y; a[6] = w.z; a[7] = w.w;
+}
+// 8 consecutive bf16 (as raw bits) from a 16-byte aligned address.
+__device__ __forceinline__ void load8(const uint16_t* p, float (&a)[8]) {
+  const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    a[2 * d] = __uint_as_float(u[d] << 16);
+    a[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA path parameters
+// ---------------------------------------------------------------------------
+constexpr int kMaxWaveSteps = 24;  // sign-word steps per branch per expand wave
+// floats per latent half: M <= 16 rows of the padded ranks of both branches
+constexpr int kTHalf = kMaxMfmaM * (kMaxRankTotal + 2 * 128);
+
+struct MfmaParams {
+  const uint32_t* V[2];
+  const uint32_t* U[2];
+  const float* g[2];
+  const float* l[2];
+  const float* h[2];
+  int R[2];
+  int RW[2];    // words per U row
+  int RWp[2];   // RW rounded up to a multiple of 4
+  int rb0[2];   // first row-block of the branch
+  int RP[2];    // padded latent row length 32 * RWp (multiple of 128)
+  int tbase[2]; // offset of the branch's [M][RP] block in t
+  int nb;
+  int M, K, KW, N;
+  int tsize;    // M * (RP[0] + RP[1]) floats
+  int nkc;      // k-chunks
+  int xvec;     // x and v2 allow 16-byte loads (aligned, K % 8 == 0)
+  const void* x;
+  const float* bias;
+  void* y;
+  float* t2;       // two halves of kTHalf floats; per branch [M][RP] latent, l-scaled
+  uint32_t* sync;  // [0] P: half the next latent kernel accumulates into
+                   // [1] Q: half the last latent kernel accumulated into
+                   // [2 + h] floats of half h that may be non-zero
+};
+
+// Latent buffer protocol (all writes idempotent, so no ordering between
+// blocks is needed; kernel boundaries order the rest):
+//   latent_mfma_kernel: h = P; accumulate into half h (which is zero);
+//     clear the first S[1-h] floats of half 1-h (making it all zero);
+//     block 0 writes Q = h and S[h] = tsize.
+//   expand_mfma_kernel: reads t from half Q; block 0 writes P = 1 - Q.
+// Calls of any shape may follow each other on one workspace; graph replay
+// works because the state lives in device memory, not in kernel arguments.
+
+// v_and_or_b32 is VOP3, which takes no literal operands on gfx9: the masks
+// live in VGPRs (pinned by an empty asm so they are not re-materialised).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+
+// Byte j of a sign word -> 8 bf16 (+1 for bit 0, -1 for bit 1); element i is
+// bit 8j+i.  Each dword holds elements 2d (low half) and 2d+1 (high half):
+// the byte is replicated into both halves (one v_mul_u32_u24 with a byte
+// select), a packed 16-bit shift moves bit 2d / 2d+1 to bit 15 of its half,
+// and (x & 0x80008000) | 0x3F803F80 makes +-1.0: 9 VALU for 8 signs.
+__device__ __forceinline__ bf16x8 signs_to_bf16x8(uint32_t word, int j, uint32_t kmask, uint32_t kone) {
+  const uint32_t b = (word >> (8 * j)) & 0xffu;
+  const uint32_t rep = b * 0x10001u;
+  const u16x2 v = __builtin_bit_cast(u16x2, rep);
+  u32x4 out;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const u16x2 sh = {(unsigned short)(15 - 2 * d), (unsigned short)(14 - 2 * d)};
+    const u16x2 r = v << sh;
+    out[d] = and_or(__builtin_bit_cast(uint32_t, r), kmask, kone);
+  }
+  return __builtin_bit_cast(bf16x8, out);
+}
+
+// hi = bf16(a), lo = bf16(a - hi) of 8 floats, two per dword in element order
+// (v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ void split8(const float (&a)[8], u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const f32x2 x = {a[2 * d], a[2 * d + 1]};
+    const bf16x2 h = __builtin_convertvector(x, bf16x2);
+    const f32x2 r = x - __builtin_convertvector(h, f32x2);
+    hi[d] = __builtin_bit_cast(uint32_t, h);
+    lo[d] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2));
+  }
+}
+
+// An MFMA A operand in LDS, compact: for each m-block (8 m), each chunk of
+// 8 k holds ROWS = 2*MR + 1 rows of 16 bytes: the hi halves of the MR
+// stored m, their lo halves, and one zero row.  MFMA lane rows (0-7 hi,
+// 8-15 lo of m = 0..7) that have no stored m read the zero row, so M = 1
+// keeps 3 rows per chunk instead of 16.  Rows of M <= m < MT hold zeros.
+template <int MT>
+struct Compact {
+  static constexpr int MB = (MT + 7) / 8;     // m-blocks
+  static constexpr int MR = MT < 8 ? MT : 8;  // stored m per block
+  static constexpr int ROWS = 2 * MR + 1;
+  // row of MFMA lane row `col` (0..15) within a chunk
+  __device__ static int lane_row(int col) {
+    const int ml = col & 7;
+    return ml < MR ? (col < 8 ? ml : MR + ml) : 2 * MR;
+  }
+};
+
+// Fill a compact operand: one thread per chunk; load_row(c, m, a) gives the
+// 8 values of chunk c for m < M.  All loads of a block are issued before any
+// is used; rows m >= M are written as zeros (their loads read row M - 1).
+template <int MT, int BLOCK, typename F>
+__device__ __forceinline__ void build_compact(u32x4* lds, int nch, int M, int tid, F&& load_row) {
+  using L = Compact<MT>;
+  for (int c = tid; c < nch; c += BLOCK) {
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb) {
+      float a[L::MR][8];
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) load_row(c, min(mb * 8 + ml, M - 1), a[ml]);
+      u32x4* base = lds + (size_t(mb) * nch + c) * L::ROWS;
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) {
+        u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+        if (mb * 8 + ml < M) split8(a[ml], hi, lo);
+        base[ml] = hi;
+        base[L::MR + ml] = lo;
+      }
+      base[2 * L::MR] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 1 (MFMA): t += l * (V_sign . (g*x)) over this block's k-chunk
+// grid.x = (row-blocks of all branches) * nkc, block = 256 threads (4 waves)
+// LDS: compact A operand of g*x for the k-chunk (KC/8 chunks)
+//
+// The k-chunks of a row-block add into t with fp32 atomics (t is zero on
+// entry); kernel completion publishes t to expand_mfma_kernel.  Atomics
+// cost nothing measurable here, unlike an agent-scope fence, which writes
+// back the whole L2 of the XCD.  The order of the additions is not fixed,
+// so the last bits of t can differ from run to run.
+// ---------------------------------------------------------------------------
+template <typename XT, int MT, int WPL>
+__global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
+  using L = Compact<MT>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  u32x4* lds_a = reinterpret_cast<u32x4*>(lds_raw);
+  constexpr int KC = 128 * WPL;
+  constexpr int NCH = KC / 8;  // 8-column chunks per k-chunk
+
+  const int rbk = int(blockIdx.x) / p.nkc;
+  const int kc = int(blockIdx.x) - rbk * p.nkc;
+  // branch selection by value (no dynamic indexing of the kernel arguments)
+  const bool b1 = p.nb > 1 && rbk >= p.rb0[1];
+  const int rb = rbk - (b1 ? p.rb0[1] : 0);
+  const int R = b1 ? p.R[1] : p.R[0];
+  const int RP = b1 ? p.RP[1] : p.RP[0];
+  const int tbase = b1 ? p.tbase[1] : 0;
+  const float* __restrict__ g = b1 ? p.g[1] : p.g[0];
+  const float* __restrict__ lvec = b1 ? p.l[1] : p.l[0];
+  const uint32_t* __restrict__ V = b1 ? p.V[1] : p.V[0];
+  const int k0 = kc * KC;
+  const int tid = int(threadIdx.x);
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int col = lane & 15;   // MFMA column = latent row within the tile
+  const int grp = lane >> 4;   // k group 0..3
+  const int r = rb * kRowBlock + wave * 16 + col;
+  const int w0 = kc * (KC / 32) + grp * WPL;
+
+  // sign words first, so that their latency overlaps the A-operand build
+  uint32_t words[WPL];
+  {
+    const uint32_t* __restrict__ vrow = V + size_t(r < R ? r : 0) * p.KW;
+#pragma unroll
+    for (int s = 0; s < WPL; ++s) {
+      const int w = w0 + s;
+      words[s] = (r < R && w < p.KW) ? vrow[w] : 0u;
+    }
+  }
+  const float lr = (r < R) ? lvec[r] : 0.f;
+  // Latent-buffer state.  Plain loads: within this launch only block 0
+  // writes sync[1] and sync[2 + h], which no block of it reads.
+  const uint32_t h = p.sync[0] & 1u;
+  const uint32_t s0 = p.sync[2];
+  const uint32_t s1 = p.sync[3];
+
+  // ---- A operand: hi/lo bf16 of g[k] * x[m, k] for this k-chunk ----
+  {
+    const XT* __restrict__ x = static_cast<const XT*>(p.x);
+    const int K = p.K;
+    const bool xvec = p.xvec != 0;
+    build_compact<MT, kBlock>(lds_a, NCH, p.M, tid, [&](int c, int m, float (&a)[8]) {
+      const int kb = k0 + 8 * c;
+      if (xvec && kb + 8 <= K) {
+        load8(x + size_t(m) * K + kb, a);
+        float gv[8];
+        load8(g + kb, gv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] *= gv[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (kb + i < K) ? g[kb + i] * to_f32(x[size_t(m) * K + kb + i]) : 0.f;
+      }
+    });
+  }
+  __syncthreads();
+
+  uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
+  asm volatile("" : "+v"(kmask), "+v"(kone));
+  const int lrow = L::lane_row(col);
+  f32x4 acc[L::MB];
+#pragma unroll
+  for (int i = 0; i < L::MB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < WPL; ++s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 bop = signs_to_bf16x8(words[s], j, kmask, kone);
+      const int c = (grp * WPL + s) * 4 + j;
+#pragma unroll
+      for (int mb = 0; mb < L::MB; ++mb) {
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, lds_a[(size_t(mb) * NCH + c) * L::ROWS + lrow]);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc[mb], 0, 0, 0);
+      }
+    }
+  }
+
+  // C rows 4*grp + i: grp 0,1 = hi of m = 4*grp + i, grp 2,3 = lo of the same m.
+  float sum[L::MB][4];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[mb][i] = acc[mb][i] + __shfl_xor(acc[mb][i], 32);
+
+  if (lane < 32 && r < R) {
+    float* trow = p.t2 + size_t(h) * kTHalf + tbase + r;
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mb * 8 + grp * 4 + i;
+        if (m < p.M) {
+          if (p.nkc == 1) trow[size_t(m) * RP] = lr * sum[mb][i];
+          else unsafeAtomicAdd(trow + size_t(m) * RP, lr * sum[mb][i]);
+        }
+      }
+  }
+
+  // clear this block's slice of the other half; publish the state
+  {
+    const uint32_t stale = h ? s0 : s1;
+    float* __restrict__ other = p.t2 + size_t(h ^ 1u) * kTHalf;
+    const int per = int((stale + gridDim.x - 1) / gridDim.x);
+    const int lo = int(blockIdx.x) * per;
+    const int hi = min(int(stale), lo + per);
+    for (int i = lo + tid; i < hi; i += kBlock) other[i] = 0.f;
+    if (blockIdx.x == 0 && tid == 0) {
+      __hip_atomic_store(p.sync + 1, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.sync + 2 + h, uint32_t(p.tsize), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b)
+// block = 2 * TILES waves covering 16 * TILES output rows: wave w owns tile
+// w % TILES (16 rows) and half w / TILES of the rank steps (4 sign words of
+// a row) of both branches; the two halves meet in LDS.  Every block reads
+// all of t, so larger M (a larger operand) takes more rows per block.
+// grid.x = ceil(N / (16 * TILES))
+// LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
+// ---------------------------------------------------------------------------
+template <int MT>
+struct ExpandShape {
+  static constexpr int TILES = MT >= 4 ? 4 : 2;
+  static constexpr int THREADS = 2 * TILES * kWave;
+  static constexpr int ROWS = 16 * TILES;
+};
+
+template <typename YT, int MT, int S>
+__global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(MfmaParams p) {
+  using L = Compact<MT>;
+  using E = ExpandShape<MT>;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  u32x4* lds_t = reinterpret_cast<u32x4*>(lds_raw);
+  __shared__ float red[E::TILES][L::MB * 4][32];
+  const int tid = int(threadIdx.x);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
+  const int lane = tid % kWave;
+  const int tile = wave % E::TILES;
+  const int half = wave / E::TILES;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int n = int(blockIdx.x) * E::ROWS + tile * 16 + col;
+  // half of the latent buffer the latent kernel of this call filled; only
+  // block 0 writes the state here, and only sync[0]
+  const uint32_t hq = p.sync[1] & 1u;
+  const bool nvalid = n < p.N;
+
+  // this wave's steps: branch 0 steps [a0, a0 + n0), branch 1 steps [c0, c0 + n1)
+  const int steps0 = p.RWp[0] / 4;
+  const int steps = steps0 + (p.nb > 1 ? p.RWp[1] / 4 : 0);
+  const int split = (steps + 1) / 2;
+  const int q0 = half ? split : 0;
+  const int q1 = half ? steps : split;
+  const int a0 = q0;
+  const int n0 = max(min(q1, steps0) - q0, 0);
+  const int c0 = max(q0, steps0) - steps0;
+  const int n1 = max(q1 - max(q0, steps0), 0);
+
+  // Sign words of the wave, unrolled over the compile-time bound S (>= n0,
+  // n1, chosen by the host), so every load is issued before the first use
+  // waits on any of them.  Every element is written on every path.
+  uint32_t pre0[S], pre1[S];
+  {
+    const int RW0 = p.RW[0];
+    const int w0 = 4 * a0 + grp;
+    const uint32_t* __restrict__ u0 = p.U[0] + size_t(nvalid ? n : 0) * RW0 + w0;
+    const int lim0 = nvalid ? RW0 - w0 : 0;  // words of this lane left in the row
+#pragma unroll
+    for (int i = 0; i < S; ++i) pre0[i] = (i < n0 && 4 * i < lim0) ? u0[4 * i] : 0u;
+    const int RW1 = p.nb > 1 ? p.RW[1] : 0;
+    const int w1 = 4 * c0 + grp;
+    const uint32_t* __restrict__ u1 = p.nb > 1 ? p.U[1] + size_t(nvalid ? n : 0) * RW1 + w1 : u0;
+    const int lim1 = (nvalid && p.nb > 1) ? RW1 - w1 : 0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) pre1[i] = (i < n1 && 4 * i < lim1) ? u1[4 * i] : 0u;
+  }
+
+  const int nch0 = 4 * p.RWp[0];
+  const int nch1 = p.nb > 1 ? 4 * p.RWp[1] : 0;
+  u32x4* tb0 = lds_t;
+  u32x4* tb1 = lds_t + size_t(L::MB) * nch0 * L::ROWS;
+  {
+    const int M = p.M;
+    const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
+    const int RP0 = p.RP[0];
+    build_compact<MT, E::THREADS>(tb0, nch0, M, tid, [&](int c, int m, float (&a)[8]) {
+      load8(ta + size_t(m) * RP0 + 8 * c, a);
+    });
+    if (p.nb > 1) {
+      const float* __restrict__ t1 = ta + p.tbase[1];
+      const int RP1 = p.RP[1];
+      build_compact<MT, E::THREADS>(tb1, nch1, M, tid, [&](int c, int m, float (&a)[8]) {
+        load8(t1 + size_t(m) * RP1 + 8 * c, a);
+      });
+    }
+  }
+  __syncthreads();
+
+  uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
+  asm volatile("" : "+v"(kmask), "+v"(kone));
+  const int lrow = L::lane_row(col);
+  f32x4 acc0[L::MB], acc1[L::MB];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb) {
+    acc0[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (i >= n0) continue;
+    const int w = 4 * (a0 + i) + grp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 bop = signs_to_bf16x8(pre0[i], j, kmask, kone);
+#pragma unroll
+      for (int mb = 0; mb < L::MB; ++mb) {
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb0[(size_t(mb) * nch0 + 4 * w + j) * L::ROWS + lrow]);
+        acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc0[mb], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    if (i >= n1) continue;
+    const int w = 4 * (c0 + i) + grp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 bop = signs_to_bf16x8(pre1[i], j, kmask, kone);
+#pragma unroll
+      for (int mb = 0; mb < L::MB; ++mb) {
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb1[(size_t(mb) * nch1 + 4 * w + j) * L::ROWS + lrow]);
+        acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc1[mb], 0, 0, 0);
+      }
+    }
+  }
+
+  // h-weighted branch sum of this half; C rows 4*grp + i (grp 0,1 hi, 2,3 lo)
+  const float h0 = nvalid ? p.h[0][n] : 0.f;
+  const float h1 = (nvalid && p.nb > 1) ? p.h[1][n] : 0.f;
+  float out[L::MB][4];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      out[mb][i] = h0 * (acc0[mb][i] + __shfl_xor(acc0[mb][i], 32)) +
+                   h1 * (acc1[mb][i] + __shfl_xor(acc1[mb][i], 32));
+
+  if (half == 1 && lane < 32) {
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[tile][mb * 4 + i][lane] = out[mb][i];
+  }
+  __syncthreads();
+  if (half == 0 && lane < 32 && nvalid) {
+    const float bn = p.bias ? p.bias[n] : 0.f;
+    YT* y = static_cast<YT*>(p.y);
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mb * 8 + grp * 4 + i;
+        if (m < p.M) store_out(y, size_t(m) * p.N + n, out[mb][i] + red[tile][mb * 4 + i][lane] + bn);
+      }
+  }
+
+  if (blockIdx.x == 0 && tid == 0) {
+    const uint32_t q = __hip_atomic_load(p.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.sync, (q & 1u) ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// General path (fp32 VALU, any M)
+// ---------------------------------------------------------------------------
 struct DevBranch {
   const uint32_t* v;  // [R, KW]
   const uint32_t* u;  // [N, RW]
@@ -52,10 +536,10 @@ struct DevBranch {
   float* t;           // workspace [M, R], l-scaled latent
   int R;
   int RW;
-  int block0;         // first latent_kernel block of this branch
+  int block0;         // first latent_valu_kernel block of this branch
 };
 
-struct FwdParams {
+struct ValuParams {
   DevBranch br[2];
   int nb;
   int M, K, KW, N;
@@ -64,34 +548,11 @@ struct FwdParams {
   void* y;
 };
 
-__device__ __forceinline__ float to_f32(float v) { return v; }
-__device__ __forceinline__ float to_f32(uint16_t v) {
-  return __uint_as_float(uint32_t(v) << 16);
-}
+__device__ __forceinline__ DevBranch pick(const ValuParams& p, int b) { return b ? p.br[1] : p.br[0]; }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
-}
-
-__device__ __forceinline__ void store_out(float* y, size_t i, float v) { y[i] = v; }
-__device__ __forceinline__ void store_out(uint16_t* y, size_t i, float v) {
-  y[i] = f32_to_bf16(v);
-}
-
-__device__ __forceinline__ DevBranch pick(const FwdParams& p, int b) {
-  return b ? p.br[1] : p.br[0];
-}
-
-// ---------------------------------------------------------------------------
-// Stage 1: t[m, r] = l[r] * sum_k sV[r, k] * g[k] * x[m, k]
-// grid.x = sum_b ceil(R_b / 4) (one wave per row), grid.y = ceil(M / MT)
-// ---------------------------------------------------------------------------
+// t[m, r]: one wave per latent row; grid.x = sum_b ceil(R_b / 4), grid.y = ceil(M / MT)
 template <typename XT, int MT>
-__global__ __launch_bounds__(kBlock) void latent_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock) void latent_valu_kernel(ValuParams p) {
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int b = (p.nb > 1 && int(blockIdx.x) >= p.br[1].block0) ? 1 : 0;
@@ -140,13 +601,10 @@ __global__ __launch_bounds__(kBlock) void latent_kernel(FwdParams p) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Stage 2: y[m, n] = bias[n] + sum_b h_b[n] * sum_r sU_b[n, r] * t_b[m, r]
-// grid.x = ceil(N / (256 / LPR)), grid.y = ceil(M / MT); LDS holds t.
-// ---------------------------------------------------------------------------
+// y[m, n]: LPR lanes per output row; grid.x = ceil(N / (256 / LPR)), grid.y = ceil(M / MT)
 template <typename YT, int MT, int LPR>
-__global__ __launch_bounds__(kBlock) void expand_kernel(FwdParams p) {
-  extern __shared__ float lds_t[];  // per branch [MT][R_b]
+__global__ __launch_bounds__(kBlock) void expand_valu_kernel(ValuParams p) {
+  extern __shared__ float lds_tv[];  // per branch [MT][R_b]
   const int m0 = int(blockIdx.y) * MT;
 
   int off = 0;
@@ -156,7 +614,7 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(FwdParams p) {
       const int mi = i / B.R;
       const int r = i - mi * B.R;
       const int m = m0 + mi;
-      lds_t[off + i] = (m < p.M) ? B.t[size_t(m) * B.R + r] : 0.f;
+      lds_tv[off + i] = (m < p.M) ? B.t[size_t(m) * B.R + r] : 0.f;
     }
     off += MT * B.R;
   }
@@ -184,7 +642,7 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(FwdParams p) {
           const bool neg = (bits >> j) & 1u;
 #pragma unroll
           for (int i = 0; i < MT; ++i) {
-            const float tv = lds_t[off + i * B.R + r0 + j];
+            const float tv = lds_tv[off + i * B.R + r0 + j];
             acc[i] += neg ? -tv : tv;
           }
         }
@@ -217,11 +675,10 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 // Sign pack / unpack (bit-exact with the reference packer)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kBlock) void unpack_kernel(const uint32_t* packed, int64_t rows,
-                                                        int64_t cols, int64_t wpr, int8_t* out) {
+__global__ __launch_bounds__(kBlock) void unpack_kernel(const uint32_t* packed, int64_t rows, int64_t cols,
+                                                        int64_t wpr, int8_t* out) {
   const int64_t total = rows * cols;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < total;
-       i += int64_t(gridDim.x) * kBlock) {
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += int64_t(gridDim.x) * kBlock) {
     const int64_t r = i / cols;
     const int64_t c = i - r * cols;
     const uint32_t word = packed[r * wpr + (c >> 5)];
@@ -229,11 +686,10 @@ __global__ __launch_bounds__(kBlock) void unpack_kernel(const uint32_t* packed, 
   }
 }
 
-__global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64_t rows,
-                                                      int64_t cols, int64_t wpr, uint32_t* out) {
+__global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64_t rows, int64_t cols,
+                                                      int64_t wpr, uint32_t* out) {
   const int64_t total = rows * wpr;
-  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < total;
-       i += int64_t(gridDim.x) * kBlock) {
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += int64_t(gridDim.x) * kBlock) {
     const int64_t r = i / wpr;
     const int64_t w = i - r * wpr;
     const int64_t c0 = w * 32;
@@ -245,6 +701,9 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
   }
 }
 
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -256,11 +715,13 @@ int check_launch(const char* what) {
 
 int validate(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N) {
   if (!branches) return set_error(LBK_ERR_ARG, "branches is NULL");
-  if (n_branches < 1 || n_branches > 2)
-    return set_error(LBK_ERR_ARG, "n_branches must be 1 or 2, got %d", n_branches);
-  if (M < 0 || M > kMaxDim) return set_error(LBK_ERR_ARG, "M must be in [0, %lld], got %lld", (long long)kMaxDim, (long long)M);
-  if (K < 1 || K > kMaxDim) return set_error(LBK_ERR_ARG, "K must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)K);
-  if (N < 1 || N > kMaxDim) return set_error(LBK_ERR_ARG, "N must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)N);
+  if (n_branches < 1 || n_branches > 2) return set_error(LBK_ERR_ARG, "n_branches must be 1 or 2, got %d", n_branches);
+  if (M < 0 || M > kMaxDim)
+    return set_error(LBK_ERR_ARG, "M must be in [0, %lld], got %lld", (long long)kMaxDim, (long long)M);
+  if (K < 1 || K > kMaxDim)
+    return set_error(LBK_ERR_ARG, "K must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)K);
+  if (N < 1 || N > kMaxDim)
+    return set_error(LBK_ERR_ARG, "N must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)N);
   int64_t rsum = 0;
   for (int b = 0; b < n_branches; ++b) {
     const lbk_branch& B = branches[b];
@@ -274,40 +735,198 @@ int validate(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, i
   return LBK_OK;
 }
 
-size_t workspace_for(const lbk_branch* branches, int n_branches, int64_t M) {
-  size_t bytes = 0;
-  for (int b = 0; b < n_branches; ++b) bytes += align256(size_t(M) * size_t(branches[b].rank) * sizeof(float));
-  return bytes;
+// Workspace layout (byte offsets), fixed so that calls of any shape on one
+// workspace keep its invariants:
+//   [0, kCounterBytes)                 counters, zero between calls
+//   [kTOffset, kTOffset + kTBytes)     MFMA-path latent halves (see MfmaParams)
+//   [kValuOffset, ...)                 general-path latent buffers
+constexpr size_t kTOffset = 4096;
+constexpr size_t kTBytes = 2 * size_t(kTHalf) * sizeof(float);
+constexpr size_t kValuOffset = kTOffset + kTBytes;
+static_assert(kCounterBytes <= kTOffset, "counter region overlaps t");
+
+// Launch plan shared by the workspace query and the forward.
+struct Plan {
+  bool mfma;
+  int mt;        // M tile of the MFMA path: 1, 2, 4, 8 or 16
+  int wpl;       // words per lane in latent_mfma_kernel
+  int nkc;       // k-chunks
+  int nrb;       // row-blocks over all branches
+  int wsteps;    // expand_mfma_kernel unroll bound S
+  size_t lds1, lds2;
+  size_t ws_total;
+};
+
+int mtile(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+
+// 16-byte rows of a compact operand with `nch` chunks
+size_t compact_rows(int mt, int64_t nch) {
+  const int mb = (mt + 7) / 8, mr = mt < 8 ? mt : 8;
+  return size_t(mb) * size_t(nch) * size_t(2 * mr + 1);
 }
 
-template <typename XT>
-void launch_latent(const FwdParams& p, int mt, dim3 grid, hipStream_t s) {
-  switch (mt) {
-    case 1: hipLaunchKernelGGL((latent_kernel<XT, 1>), grid, dim3(kBlock), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((latent_kernel<XT, 2>), grid, dim3(kBlock), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((latent_kernel<XT, 4>), grid, dim3(kBlock), 0, s, p); break;
-    default: hipLaunchKernelGGL((latent_kernel<XT, 8>), grid, dim3(kBlock), 0, s, p); break;
+Plan make_plan(const lbk_branch* br, int nb, int64_t M, int64_t K) {
+  Plan pl{};
+  int64_t rwp_sum = 0, nrb = 0;
+  for (int b = 0; b < nb; ++b) {
+    rwp_sum += ceil_div(ceil_div(br[b].rank, 32), 4) * 4;
+    nrb += ceil_div(br[b].rank, kRowBlock);
+  }
+  pl.nrb = int(nrb);
+  pl.mt = mtile(M);
+  const size_t lds2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
+  const int64_t wave_steps = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
+  pl.mfma = (M >= 1 && M <= kMaxMfmaM && lds2 <= size_t(kMaxLds) && wave_steps <= kMaxWaveSteps);
+  if (pl.mfma) {
+    // enough blocks to cover the CUs, short per-wave chains
+    pl.wpl = 2;
+    for (int w : {8, 4}) {
+      if (nrb * ceil_div(K, 128 * w) >= 256) { pl.wpl = w; break; }
+    }
+    pl.nkc = int(ceil_div(K, 128 * pl.wpl));
+    pl.wsteps = wave_steps <= 4 ? 4 : wave_steps <= 8 ? 8 : wave_steps <= 16 ? 16 : 24;
+    pl.lds1 = compact_rows(pl.mt, 128 * pl.wpl / 8) * 16;
+    pl.lds2 = lds2;
+    pl.ws_total = kTOffset + kTBytes;
+  } else {
+    size_t bytes = kValuOffset;
+    for (int b = 0; b < nb; ++b) bytes += align256(size_t(M) * size_t(br[b].rank) * sizeof(float));
+    pl.ws_total = bytes;
+  }
+  return pl;
+}
+
+template <typename XT, int MT, int WPL>
+void launch_latent_mfma(const MfmaParams& p, int grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((latent_mfma_kernel<XT, MT, WPL>), dim3(grid), dim3(kBlock), lds, s, p);
+}
+
+template <typename XT, int MT>
+void dispatch_latent_wpl(const MfmaParams& p, int wpl, int grid, size_t lds, hipStream_t s) {
+  switch (wpl) {
+    case 8: launch_latent_mfma<XT, MT, 8>(p, grid, lds, s); break;
+    case 4: launch_latent_mfma<XT, MT, 4>(p, grid, lds, s); break;
+    default: launch_latent_mfma<XT, MT, 2>(p, grid, lds, s); break;
   }
 }
 
+template <typename XT>
+void dispatch_latent(const MfmaParams& p, const Plan& pl, int grid, hipStream_t s) {
+  switch (pl.mt) {
+    case 1: dispatch_latent_wpl<XT, 1>(p, pl.wpl, grid, pl.lds1, s); break;
+    case 2: dispatch_latent_wpl<XT, 2>(p, pl.wpl, grid, pl.lds1, s); break;
+    case 4: dispatch_latent_wpl<XT, 4>(p, pl.wpl, grid, pl.lds1, s); break;
+    case 8: dispatch_latent_wpl<XT, 8>(p, pl.wpl, grid, pl.lds1, s); break;
+    default: dispatch_latent_wpl<XT, 16>(p, pl.wpl, grid, pl.lds1, s); break;
+  }
+}
+
+template <typename YT, int MT, int S>
+void launch_expand_mfma_s(const MfmaParams& p, int /*unused*/, size_t lds, hipStream_t s) {
+  using E = ExpandShape<MT>;
+  const int grid = int(ceil_div(p.N, E::ROWS));
+  hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S>), dim3(grid), dim3(E::THREADS), lds, s, p);
+}
+
 template <typename YT, int MT>
-void launch_expand_lpr(const FwdParams& p, int lpr, size_t lds, hipStream_t s) {
-  const int rows = kBlock / lpr;
-  const dim3 grid{unsigned(ceil_div(p.N, rows)), unsigned(ceil_div(p.M, MT)), 1u};
-  switch (lpr) {
-    case 4: hipLaunchKernelGGL((expand_kernel<YT, MT, 4>), grid, dim3(kBlock), lds, s, p); break;
-    case 16: hipLaunchKernelGGL((expand_kernel<YT, MT, 16>), grid, dim3(kBlock), lds, s, p); break;
-    default: hipLaunchKernelGGL((expand_kernel<YT, MT, 64>), grid, dim3(kBlock), lds, s, p); break;
+void dispatch_expand_s(const MfmaParams& p, int wsteps, int grid, size_t lds, hipStream_t s) {
+  switch (wsteps) {
+    case 4: launch_expand_mfma_s<YT, MT, 4>(p, grid, lds, s); break;
+    case 8: launch_expand_mfma_s<YT, MT, 8>(p, grid, lds, s); break;
+    case 16: launch_expand_mfma_s<YT, MT, 16>(p, grid, lds, s); break;
+    default: launch_expand_mfma_s<YT, MT, kMaxWaveSteps>(p, grid, lds, s); break;
   }
 }
 
 template <typename YT>
-void launch_expand(const FwdParams& p, int mt, int lpr, size_t lds, hipStream_t s) {
+void dispatch_expand(const MfmaParams& p, const Plan& pl, int grid, hipStream_t s) {
+  switch (pl.mt) {
+    case 1: dispatch_expand_s<YT, 1>(p, pl.wsteps, grid, pl.lds2, s); break;
+    case 2: dispatch_expand_s<YT, 2>(p, pl.wsteps, grid, pl.lds2, s); break;
+    case 4: dispatch_expand_s<YT, 4>(p, pl.wsteps, grid, pl.lds2, s); break;
+    case 8: dispatch_expand_s<YT, 8>(p, pl.wsteps, grid, pl.lds2, s); break;
+    default: dispatch_expand_s<YT, 16>(p, pl.wsteps, grid, pl.lds2, s); break;
+  }
+}
+
+int forward_mfma(const lbk_branch* branches, int nb, const Plan& pl, int64_t M, int64_t K, int64_t N,
+                 const void* x, int x_dtype, const float* bias, void* y, int y_dtype, void* workspace,
+                 hipStream_t s) {
+  MfmaParams p;
+  memset(&p, 0, sizeof(p));
+  p.nb = nb;
+  p.M = int(M);
+  p.K = int(K);
+  p.KW = int(ceil_div(K, 32));
+  p.N = int(N);
+  int rb = 0, tbase = 0;
+  for (int b = 0; b < nb; ++b) {
+    const lbk_branch& S = branches[b];
+    p.V[b] = reinterpret_cast<const uint32_t*>(S.v_sign);
+    p.U[b] = reinterpret_cast<const uint32_t*>(S.u_sign);
+    p.g[b] = S.v2;
+    p.l[b] = S.mid;
+    p.h[b] = S.u1;
+    p.R[b] = int(S.rank);
+    p.RW[b] = int(ceil_div(S.rank, 32));
+    p.RWp[b] = int(ceil_div(p.RW[b], 4) * 4);
+    p.rb0[b] = rb;
+    p.RP[b] = 32 * p.RWp[b];
+    p.tbase[b] = tbase;
+    rb += int(ceil_div(S.rank, kRowBlock));
+    tbase += int(M) * p.RP[b];
+  }
+  p.tsize = tbase;
+  p.nkc = pl.nkc;
+  p.x = x;
+  p.bias = bias;
+  p.y = y;
+  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  for (int b = 0; b < nb; ++b) xvec = xvec && (reinterpret_cast<uintptr_t>(branches[b].v2) % 16) == 0;
+  p.xvec = xvec ? 1 : 0;
+  char* ws = static_cast<char*>(workspace);
+  p.sync = reinterpret_cast<uint32_t*>(ws);
+  p.t2 = reinterpret_cast<float*>(ws + kTOffset);
+
+  const int grid1 = pl.nrb * pl.nkc;
+  if (x_dtype == LBK_F32) dispatch_latent<float>(p, pl, grid1, s);
+  else dispatch_latent<uint16_t>(p, pl, grid1, s);
+  int rc = check_launch("latent_mfma_kernel");
+  if (rc != LBK_OK) return rc;
+
+  if (y_dtype == LBK_F32) dispatch_expand<float>(p, pl, 0, s);
+  else dispatch_expand<uint16_t>(p, pl, 0, s);
+  return check_launch("expand_mfma_kernel");
+}
+
+template <typename XT>
+void launch_latent_valu(const ValuParams& p, int mt, dim3 grid, hipStream_t s) {
   switch (mt) {
-    case 1: launch_expand_lpr<YT, 1>(p, lpr, lds, s); break;
-    case 2: launch_expand_lpr<YT, 2>(p, lpr, lds, s); break;
-    case 4: launch_expand_lpr<YT, 4>(p, lpr, lds, s); break;
-    default: launch_expand_lpr<YT, 8>(p, lpr, lds, s); break;
+    case 1: hipLaunchKernelGGL((latent_valu_kernel<XT, 1>), grid, dim3(kBlock), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((latent_valu_kernel<XT, 2>), grid, dim3(kBlock), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((latent_valu_kernel<XT, 4>), grid, dim3(kBlock), 0, s, p); break;
+    default: hipLaunchKernelGGL((latent_valu_kernel<XT, 8>), grid, dim3(kBlock), 0, s, p); break;
+  }
+}
+
+template <typename YT, int MT>
+void launch_expand_valu_lpr(const ValuParams& p, int lpr, size_t lds, hipStream_t s) {
+  const int rows = kBlock / lpr;
+  const dim3 grid{unsigned(ceil_div(p.N, rows)), unsigned(ceil_div(p.M, MT)), 1u};
+  switch (lpr) {
+    case 4: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 4>), grid, dim3(kBlock), lds, s, p); break;
+    case 16: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 16>), grid, dim3(kBlock), lds, s, p); break;
+    default: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 64>), grid, dim3(kBlock), lds, s, p); break;
+  }
+}
+
+template <typename YT>
+void launch_expand_valu(const ValuParams& p, int mt, int lpr, size_t lds, hipStream_t s) {
+  switch (mt) {
+    case 1: launch_expand_valu_lpr<YT, 1>(p, lpr, lds, s); break;
+    case 2: launch_expand_valu_lpr<YT, 2>(p, lpr, lds, s); break;
+    case 4: launch_expand_valu_lpr<YT, 4>(p, lpr, lds, s); break;
+    default: launch_expand_valu_lpr<YT, 8>(p, lpr, lds, s); break;
   }
 }
 
@@ -317,37 +936,11 @@ int mtile_for(int64_t M, int64_t cap) {
   return mt;
 }
 
-}  // namespace
-
-extern "C" {
-
-int lbk_abi_version(void) { return LBK_ABI_VERSION; }
-
-const char* lbk_last_error(void) { return g_last_error; }
-
-size_t lbk_linear_workspace_bytes(const lbk_branch* branches, int n_branches, int64_t M, int64_t K,
-                                  int64_t N) {
-  if (validate(branches, n_branches, M, K, N) != LBK_OK) return 0;
-  return workspace_for(branches, n_branches, M);
-}
-
-int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N,
-                       const void* x, int x_dtype, const float* bias, void* y, int y_dtype,
-                       void* workspace, size_t workspace_bytes, void* stream) {
-  g_last_error[0] = '\0';
-  int rc = validate(branches, n_branches, M, K, N);
-  if (rc != LBK_OK) return rc;
-  if (x_dtype != LBK_F32 && x_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "x_dtype %d unsupported", x_dtype);
-  if (y_dtype != LBK_F32 && y_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "y_dtype %d unsupported", y_dtype);
-  if (M == 0) return LBK_OK;
-  if (!x || !y) return set_error(LBK_ERR_ARG, "x or y is NULL");
-  const size_t need = workspace_for(branches, n_branches, M);
-  if (!workspace || workspace_bytes < need)
-    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-
-  FwdParams p;
+int forward_valu(const lbk_branch* branches, int nb, int64_t M, int64_t K, int64_t N, const void* x,
+                 int x_dtype, const float* bias, void* y, int y_dtype, void* workspace, hipStream_t s) {
+  ValuParams p;
   memset(&p, 0, sizeof(p));
-  p.nb = n_branches;
+  p.nb = nb;
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
@@ -355,11 +948,11 @@ int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, in
   p.x = x;
   p.bias = bias;
   p.y = y;
-  char* ws = static_cast<char*>(workspace);
+  char* ws = static_cast<char*>(workspace) + kValuOffset;  // counters and t stay untouched
   int blocks = 0;
   int64_t rsum = 0;
   int rw_max = 0;
-  for (int b = 0; b < n_branches; ++b) {
+  for (int b = 0; b < nb; ++b) {
     const lbk_branch& S = branches[b];
     DevBranch& D = p.br[b];
     D.v = reinterpret_cast<const uint32_t*>(S.v_sign);
@@ -376,31 +969,61 @@ int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, in
     rsum += S.rank;
     if (D.RW > rw_max) rw_max = D.RW;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-
   const int mt1 = mtile_for(M, 8);
   const int64_t mchunks1 = ceil_div(M, mt1);
   if (mchunks1 > 65535) return set_error(LBK_ERR_ARG, "M=%lld too large for this path", (long long)M);
   const dim3 g1{unsigned(blocks), unsigned(mchunks1), 1u};
-  if (x_dtype == LBK_F32) launch_latent<float>(p, mt1, g1, s);
-  else launch_latent<uint16_t>(p, mt1, g1, s);
-  rc = check_launch("latent_kernel");
+  if (x_dtype == LBK_F32) launch_latent_valu<float>(p, mt1, g1, s);
+  else launch_latent_valu<uint16_t>(p, mt1, g1, s);
+  int rc = check_launch("latent_valu_kernel");
   if (rc != LBK_OK) return rc;
 
-  const int64_t cap = kLdsBudget / (rsum * int64_t(sizeof(float)));
+  const int64_t cap = kValuLdsBudget / (rsum * int64_t(sizeof(float)));
   const int mt2 = mtile_for(M, cap < 1 ? 1 : cap);
   if (ceil_div(M, mt2) > 65535) return set_error(LBK_ERR_ARG, "M=%lld too large for this path", (long long)M);
   const size_t lds = size_t(rsum) * mt2 * sizeof(float);
   const int lpr = rw_max <= 8 ? 4 : (rw_max <= 32 ? 16 : 64);
-  if (y_dtype == LBK_F32) launch_expand<float>(p, mt2, lpr, lds, s);
-  else launch_expand<uint16_t>(p, mt2, lpr, lds, s);
-  return check_launch("expand_kernel");
+  if (y_dtype == LBK_F32) launch_expand_valu<float>(p, mt2, lpr, lds, s);
+  else launch_expand_valu<uint16_t>(p, mt2, lpr, lds, s);
+  return check_launch("expand_valu_kernel");
 }
 
-int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const int32_t* v_sign,
-                         int64_t v_cols, const float* mid, const int32_t* u_sign, int64_t u_cols,
-                         const float* u1, int64_t out_features, float* output, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+}  // namespace
+
+extern "C" {
+
+int lbk_abi_version(void) { return LBK_ABI_VERSION; }
+
+const char* lbk_last_error(void) { return g_last_error; }
+
+size_t lbk_linear_workspace_bytes(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N) {
+  if (validate(branches, n_branches, M, K, N) != LBK_OK) return 0;
+  return make_plan(branches, n_branches, M, K).ws_total;
+}
+
+int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N,
+                       const void* x, int x_dtype, const float* bias, void* y, int y_dtype, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  int rc = validate(branches, n_branches, M, K, N);
+  if (rc != LBK_OK) return rc;
+  if (x_dtype != LBK_F32 && x_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "x_dtype %d unsupported", x_dtype);
+  if (y_dtype != LBK_F32 && y_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "y_dtype %d unsupported", y_dtype);
+  if (M == 0) return LBK_OK;
+  if (!x || !y) return set_error(LBK_ERR_ARG, "x or y is NULL");
+  const Plan pl = make_plan(branches, n_branches, M, K);
+  if (!workspace || workspace_bytes < pl.ws_total)
+    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.mfma)
+    return forward_mfma(branches, n_branches, pl, M, K, N, x, x_dtype, bias, y, y_dtype, workspace, s);
+  return forward_valu(branches, n_branches, M, K, N, x, x_dtype, bias, y, y_dtype, workspace, s);
+}
+
+int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const int32_t* v_sign, int64_t v_cols,
+                         const float* mid, const int32_t* u_sign, int64_t u_cols, const float* u1,
+                         int64_t out_features, float* output, void* workspace, size_t workspace_bytes,
+                         void* stream) {
   lbk_branch b;
   b.v_sign = v_sign;
   b.u_sign = u_sign;
@@ -408,8 +1031,8 @@ int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const i
   b.mid = mid;
   b.u1 = u1;
   b.rank = u_cols;
-  return lbk_linear_forward(&b, 1, M, v_cols, out_features, input, LBK_F32, nullptr, output, LBK_F32,
-                            workspace, workspace_bytes, stream);
+  return lbk_linear_forward(&b, 1, M, v_cols, out_features, input, LBK_F32, nullptr, output, LBK_F32, workspace,
+                            workspace_bytes, stream);
 }
 
 int lbk_unpack_signs(const int32_t* packed, int64_t rows, int64_t cols, int8_t* out, void* stream) {
@@ -432,8 +1055,8 @@ int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols, int32_t* out
   const int64_t wpr = ceil_div(cols, 32);
   const int64_t total = rows * wpr;
   const int64_t blocks = ceil_div(total, kBlock) < 65536 ? ceil_div(total, kBlock) : 65536;
-  hipLaunchKernelGGL(pack_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
-                     signs, rows, cols, wpr, reinterpret_cast<uint32_t*>(out));
+  hipLaunchKernelGGL(pack_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), signs,
+                     rows, cols, wpr, reinterpret_cast<uint32_t*>(out));
   return check_launch("pack_kernel");
 }
 

@@ -33,14 +33,22 @@ _DTYPE_CODES = {torch.float32: _lib.LBK_F32, torch.bfloat16: _lib.LBK_BF16}
 
 # (device index, stream handle) -> uint8 workspace tensor
 _workspaces: Dict[Tuple[int, int], torch.Tensor] = {}
+# Outgrown workspaces stay allocated: a captured graph may still use them.
+_retired: list = []
 
 
 def workspace_for(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """Per-(device, stream) scratch buffer, grown on demand and kept."""
+    """Per-(device, stream) scratch buffer, grown on demand and kept.
+
+    It starts zeroed: the library keeps arrival counters at its head that
+    must read zero before a call and that every call leaves at zero.
+    """
     key = (device.index if device.index is not None else torch.cuda.current_device(), int(stream))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        if ws is not None:
+            _retired.append(ws)
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
