@@ -1,0 +1,276 @@
+"""Benchmark of the LittleBitLinear forward on one MI355X.
+
+Workload: the Llama-2-7B-shaped 0.1-BPW draft decode
+step -- the 7 projections of each of 32 decoder layers at batch 1 (q, k, v, o
+4096->4096 rank 205; gate, up 4096->11008 rank 298; down 11008->4096 rank
+298), fp32 activations, random packed signs and |N(0,1)|+0.05 scales.  One
+step = the 224 forwards in decode order, captured as one HIP graph.
+
+value = algorithmic bytes of a step / time of a step, with the weights cold:
+the step rotates over enough weight replicas that the working set exceeds
+the 256 MB Infinity Cache.  The warm figure (one replica) is reported too.
+
+roofline = the dominant projection class (largest share of the step), one
+forward = the two kernels (latent + expand) and the gap between them, timed
+with HIP events around a graph of 32 back-to-back forwards of the class;
+bytes per forward from the BASELINE formula.  cpu_baseline = the reference AVX2 kernel littlebit_linear
+(oracle/_ref, built from the reference source) on the host cores, over a
+bounded number of whole steps.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "µs/layer + achieved GB/s (LittleBitLinear GEMV); draft tok/s, Llama-2-7B 0.1BPW"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def proj_bytes(M, K, N, ranks, sx=4, sy=4):
+    """Algorithmic bytes of one forward (BASELINE formula)."""
+    b = 0
+    for R in ranks:
+        b += R * math.ceil(K / 32) * 4 + N * math.ceil(R / 32) * 4 + 4 * (K + R + N)
+    return b + M * K * sx + M * N * sy
+
+
+def draft_layer_shapes():
+    from littlebit_amd.synthetic import llama_projection_shapes
+    return llama_projection_shapes(residual=False)
+
+
+def make_device_branch(gen, K, R, N, dev):
+    import torch
+    from littlebit_amd import LittleBitBranch
+
+    def words(rows, cols):
+        wpr = (cols + 31) // 32
+        w = torch.randint(-2**31, 2**31, (rows, wpr), generator=gen, dtype=torch.int64, device="cpu")
+        tail = cols - 32 * (wpr - 1)
+        if tail < 32:
+            w[:, -1] &= (1 << tail) - 1
+        return w.to(torch.int32).to(dev)
+
+    def scales(n):
+        return (torch.randn(n, generator=gen).abs() + 0.05).to(dev)
+
+    return LittleBitBranch(v_sign=words(R, K), u_sign=words(N, R), v2=scales(K), mid=scales(R), u1=scales(N))
+
+
+class DraftStep:
+    """One replica of the 224 projections and their inputs/outputs."""
+
+    def __init__(self, gen, dev, layers):
+        import torch
+        from littlebit_amd import LittleBitProjection
+        self.items = []
+        for _ in range(layers):
+            for name, K, N, ranks in draft_layer_shapes():
+                proj = LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
+                x = torch.randn((1, K), generator=gen).to(dev)
+                y = torch.empty((1, N), device=dev)
+                self.items.append((name, proj, x, y))
+
+    def run(self):
+        for _, proj, x, y in self.items:
+            proj.forward(x, out=y)
+
+
+def capture(fn, stream):
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()  # warm: sizes this stream's workspace outside the capture
+    stream.synchronize()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    return g
+
+
+def time_graphs(graphs, steps, warmup, stream):
+    import torch
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def class_items(gen, dev, name, count):
+    """`count` projections of one class (distinct weights) with inputs/outputs."""
+    import torch
+    from littlebit_amd import LittleBitProjection
+    _, K, N, ranks = next(s for s in draft_layer_shapes() if s[0] == name)
+    items = []
+    for _ in range(count):
+        proj = LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
+        items.append((proj, torch.randn((1, K), generator=gen).to(dev), torch.empty((1, N), device=dev)))
+    return K, N, ranks, items
+
+
+def forward_duration_us(gen, dev, name, stream, count=32, steps=100, warmup=10):
+    """Duration of one forward (latent + expand kernels and the gap between
+    them) in a HIP graph of `count` back-to-back forwards of one class, from
+    HIP events on the launch stream around the graph replays."""
+    K, N, ranks, items = class_items(gen, dev, name, count)
+    g = capture(lambda: [p.forward(x, out=y) for p, x, y in items], stream)
+    ms = time_graphs([g], steps, warmup, stream)
+    return K, N, ranks, ms * 1000.0 / count
+
+
+def cpu_baseline(layers, budget_s=12.0):
+    """The reference littlebit_linear (int8-quantised AVX2) over whole draft
+    steps on the host cores, within a time budget."""
+    import torch
+    try:
+        from oracle import build_ref  # checker / baseline only
+        ops = build_ref.load()
+    except Exception as e:  # noqa: BLE001
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference",
+                "sample": f"unavailable: {e}"}
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
+    step = []
+    for _ in range(layers):
+        for name, K, N, ranks in draft_layer_shapes():
+            R = ranks[0]
+            b = make_device_branch(gen, K, R, N, "cpu")
+            x = torch.randn((1, K), generator=gen)
+            step.append((K, N, R, x, b))
+    step_bytes = sum(proj_bytes(1, K, N, [R]) for K, N, R, _, _ in step)
+
+    def one_step():
+        for K, N, R, x, b in step:
+            ops.littlebit_linear(x, b.v2.reshape(1, K), b.v_sign, K, b.mid.reshape(1, R), b.u_sign, R,
+                                 b.u1.reshape(1, N))
+
+    one_step()
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        one_step()
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 100000:
+            break
+    ms_step = el / steps * 1000.0
+    return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "ms_per_step": round(ms_step, 3), "tok_per_s_linears": round(1000.0 / ms_step, 2),
+            "sample": (f"littlebit_cpu_ops::littlebit_linear (reference AVX2 kernel, int8 activations) over "
+                       f"{steps} whole draft steps ({layers} layers x 7 projections, distinct weights, "
+                       f"{step_bytes / 2**20:.0f} MiB per step) in {el:.1f} s; torch intra-op threads = {threads}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--only", choices=["attn", "gate", "down"], default=None,
+                    help="profiling aid: replay only this projection class (32 per graph) and print its timing")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build uses no collectives); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import littlebit_amd._lib as L
+    L.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream()
+
+    gen = torch.Generator().manual_seed(1002)
+    if args.only:
+        name = {"attn": "q_proj", "gate": "gate_proj", "down": "down_proj"}[args.only]
+        K, N, ranks, us = forward_duration_us(gen, dev, name, stream, args.layers, args.steps, args.warmup)
+        b = proj_bytes(1, K, N, ranks)
+        print(json.dumps({"only": args.only, "K": K, "N": N, "ranks": ranks, "us_per_forward_in_graph": round(us, 3),
+                          "bytes_per_forward": b, "gbs": round(b / us / 1e3, 2)}))
+        return
+    first = DraftStep(gen, dev, args.layers)
+    step_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) for _, p, _, _ in first.items)
+    weight_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) - 4 * (p.in_features + p.out_features)
+                       for _, p, _, _ in first.items)
+    replicas = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
+    steps_list = [first] + [DraftStep(gen, dev, args.layers) for _ in range(replicas - 1)]
+    graphs = [capture(s.run, stream) for s in steps_list]
+
+    ms_cold = time_graphs(graphs, args.steps, args.warmup, stream)
+    ms_warm = time_graphs(graphs[:1], args.steps, args.warmup, stream)
+
+    # per projection class: forward duration in a graph of back-to-back forwards
+    classes = {"attn 4096->4096 R205": "q_proj", "gate/up 4096->11008 R298": "gate_proj",
+               "down 11008->4096 R298": "down_proj"}
+    per_layer_count = {"attn 4096->4096 R205": 4, "gate/up 4096->11008 R298": 2, "down 11008->4096 R298": 1}
+    cls_stats = {}
+    for cname, name in classes.items():
+        K, N, ranks, us = forward_duration_us(gen, dev, name, stream)
+        b = proj_bytes(1, K, N, ranks)
+        cls_stats[cname] = {"us_per_forward": round(us, 3), "bytes": b, "gbs": b / us / 1e3,
+                            "share_us_per_layer": us * per_layer_count[cname]}
+    dom = max(cls_stats, key=lambda c: cls_stats[c]["share_us_per_layer"])
+    d = cls_stats[dom]
+    roofline = {"bound": "hbm", "achieved": round(d["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": None,
+                "kernel": f"LittleBitLinear forward ({dom}): latent_mfma_kernel + expand_mfma_kernel",
+                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_forward"]}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.layers, args.cpu_budget)
+    value = step_bytes / (ms_cold * 1e-3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_cold, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "llama2-7b-draft-0.1bpw-decode-step (224 LittleBitLinear forwards, M=1)",
+                   "layers": args.layers, "hidden": 4096, "intermediate": 11008,
+                   "ranks": {"attn": 205, "mlp": 298}, "batch": 1, "activations": "fp32",
+                   "bytes_per_step": step_bytes, "weight_bytes_per_step": weight_bytes,
+                   "cache": f"cold: {replicas} weight replicas rotated ({replicas * weight_bytes / 2**20:.0f} MiB "
+                            f"> 256 MiB Infinity Cache)", "graph": "one HIP graph per step"},
+        "us_per_layer": round(ms_cold * 1000.0 / args.layers, 3),
+        "tok_per_s_linears": round(1000.0 / ms_cold, 2),
+        "warm": {"ms_per_step": round(ms_warm, 4), "value": round(step_bytes / (ms_warm * 1e-3) / 1e9, 3),
+                 "us_per_layer": round(ms_warm * 1000.0 / args.layers, 3)},
+        "per_class": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                      for k, v in cls_stats.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
