@@ -4,16 +4,18 @@ Workload: the Llama-2-7B-shaped 0.1-BPW draft decode
 step -- the 7 projections of each of 32 decoder layers at batch 1 (q, k, v, o
 4096->4096 rank 205; gate, up 4096->11008 rank 298; down 11008->4096 rank
 298), fp32 activations, random packed signs and |N(0,1)|+0.05 scales.  One
-step = the 224 forwards in decode order, captured as one HIP graph.
+step = the 224 forwards in decode order, captured as one HIP graph; per layer
+four calls: q/k/v as one group call (they read the same input), o, gate/up as
+one group call, down -- two kernel launches per call.
 
 value = algorithmic bytes of a step / time of a step, with the weights cold:
 the step rotates over enough weight replicas that the working set exceeds
 the 256 MB Infinity Cache.  The warm figure (one replica) is reported too.
 
-roofline = the dominant projection class (largest share of the step), one
-forward = the two kernels (latent + expand) and the gap between them, timed
-with HIP events around a graph of 32 back-to-back forwards of the class;
-bytes per forward from the BASELINE formula.  cpu_baseline = the reference AVX2 kernel littlebit_linear
+roofline = the call kind with the longest duration, one call = its two
+kernels (latent + expand) and the gap between them, timed with HIP events
+around a graph of 32 back-to-back calls of that kind; bytes per call from
+the BASELINE formula, summed over the call's projections.  cpu_baseline = the reference AVX2 kernel littlebit_linear
 (oracle/_ref, built from the reference source) on the host cores, over a
 bounded number of whole steps.
 
@@ -69,23 +71,58 @@ def make_device_branch(gen, K, R, N, dev):
     return LittleBitBranch(v_sign=words(R, K), u_sign=words(N, R), v2=scales(K), mid=scales(R), u1=scales(N))
 
 
-class DraftStep:
-    """One replica of the 224 projections and their inputs/outputs."""
+# One decoder layer's linears as launches: projections reading the same input
+# run as one group call (q/k/v, gate/up), the others alone.
+LAYER_CALLS = [("qkv", ("q_proj", "k_proj", "v_proj")), ("o", ("o_proj",)),
+               ("gate/up", ("gate_proj", "up_proj")), ("down", ("down_proj",))]
 
-    def __init__(self, gen, dev, layers):
+
+class Call:
+    """One launch pair: a projection or a group of projections with a shared
+    input, its input x [1, K] and outputs."""
+
+    def __init__(self, gen, dev, names, grouped=True):
         import torch
-        from littlebit_amd import LittleBitProjection
-        self.items = []
-        for _ in range(layers):
-            for name, K, N, ranks in draft_layer_shapes():
-                proj = LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
-                x = torch.randn((1, K), generator=gen).to(dev)
-                y = torch.empty((1, N), device=dev)
-                self.items.append((name, proj, x, y))
+        from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+        shapes = {s[0]: s for s in draft_layer_shapes()}
+        self.names = names
+        self.projs = []
+        for nm in names:
+            _, K, N, ranks = shapes[nm]
+            self.projs.append(LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks]))
+        self.K = self.projs[0].in_features
+        self.x = torch.randn((1, self.K), generator=gen).to(dev)
+        self.outs = [torch.empty((1, p.out_features), device=dev) for p in self.projs]
+        self.group = LittleBitProjectionGroup(self.projs) if grouped and len(self.projs) > 1 else None
+        self.bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) for p in self.projs)
+        self.weight_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks)
+                                - 4 * (p.in_features + p.out_features) for p in self.projs)
 
     def run(self):
-        for _, proj, x, y in self.items:
-            proj.forward(x, out=y)
+        if self.group is not None:
+            self.group.forward(self.x, outs=self.outs)
+        else:
+            for p, o in zip(self.projs, self.outs):
+                p.forward(self.x, out=o)
+
+
+class DraftStep:
+    """One replica of a step's 224 projections (32 layers x 7) as calls."""
+
+    def __init__(self, gen, dev, layers, grouped=True):
+        self.calls = [Call(gen, dev, names, grouped) for _ in range(layers) for _, names in LAYER_CALLS]
+
+    @property
+    def bytes(self):
+        return sum(c.bytes for c in self.calls)
+
+    @property
+    def weight_bytes(self):
+        return sum(c.weight_bytes for c in self.calls)
+
+    def run(self):
+        for c in self.calls:
+            c.run()
 
 
 def capture(fn, stream):
@@ -114,26 +151,15 @@ def time_graphs(graphs, steps, warmup, stream):
     return start.elapsed_time(end) / steps  # ms per step
 
 
-def class_items(gen, dev, name, count):
-    """`count` projections of one class (distinct weights) with inputs/outputs."""
-    import torch
-    from littlebit_amd import LittleBitProjection
-    _, K, N, ranks = next(s for s in draft_layer_shapes() if s[0] == name)
-    items = []
-    for _ in range(count):
-        proj = LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
-        items.append((proj, torch.randn((1, K), generator=gen).to(dev), torch.empty((1, N), device=dev)))
-    return K, N, ranks, items
-
-
-def forward_duration_us(gen, dev, name, stream, count=32, steps=100, warmup=10):
-    """Duration of one forward (latent + expand kernels and the gap between
-    them) in a HIP graph of `count` back-to-back forwards of one class, from
-    HIP events on the launch stream around the graph replays."""
-    K, N, ranks, items = class_items(gen, dev, name, count)
-    g = capture(lambda: [p.forward(x, out=y) for p, x, y in items], stream)
+def call_duration_us(gen, dev, names, stream, count=32, steps=100, warmup=10):
+    """Duration of one call (its latent + expand kernels and the gap between
+    them) in a HIP graph of `count` back-to-back calls of one kind with
+    distinct weights, from HIP events on the launch stream around the
+    graph replays.  Returns (call, microseconds)."""
+    calls = [Call(gen, dev, names) for _ in range(count)]
+    g = capture(lambda: [c.run() for c in calls], stream)
     ms = time_graphs([g], steps, warmup, stream)
-    return K, N, ranks, ms * 1000.0 / count
+    return calls[0], ms * 1000.0 / count
 
 
 def cpu_baseline(layers, budget_s=12.0):
@@ -188,8 +214,8 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--only", choices=["attn", "gate", "down"], default=None,
-                    help="profiling aid: replay only this projection class (32 per graph) and print its timing")
+    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down"], default=None,
+                    help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build uses no collectives); got --gpus {args.gpus}",
@@ -204,40 +230,39 @@ def main():
     stream = torch.cuda.Stream()
 
     gen = torch.Generator().manual_seed(1002)
+    kinds = dict(LAYER_CALLS)
     if args.only:
-        name = {"attn": "q_proj", "gate": "gate_proj", "down": "down_proj"}[args.only]
-        K, N, ranks, us = forward_duration_us(gen, dev, name, stream, args.layers, args.steps, args.warmup)
-        b = proj_bytes(1, K, N, ranks)
-        print(json.dumps({"only": args.only, "K": K, "N": N, "ranks": ranks, "us_per_forward_in_graph": round(us, 3),
-                          "bytes_per_forward": b, "gbs": round(b / us / 1e3, 2)}))
+        names = kinds[args.only.replace("gate_up", "gate/up")]
+        call, us = call_duration_us(gen, dev, names, stream, args.layers, args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "projections": list(names), "us_per_call_in_graph": round(us, 3),
+                          "bytes_per_call": call.bytes, "gbs": round(call.bytes / us / 1e3, 2)}))
         return
     first = DraftStep(gen, dev, args.layers)
-    step_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) for _, p, _, _ in first.items)
-    weight_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) - 4 * (p.in_features + p.out_features)
-                       for _, p, _, _ in first.items)
+    step_bytes, weight_bytes = first.bytes, first.weight_bytes
     replicas = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
     steps_list = [first] + [DraftStep(gen, dev, args.layers) for _ in range(replicas - 1)]
     graphs = [capture(s.run, stream) for s in steps_list]
-
     ms_cold = time_graphs(graphs, args.steps, args.warmup, stream)
     ms_warm = time_graphs(graphs[:1], args.steps, args.warmup, stream)
+    del graphs, steps_list, first
+    # the same step with every projection launched on its own (no groups)
+    single = [DraftStep(gen, dev, args.layers, grouped=False) for _ in range(replicas)]
+    graphs = [capture(s.run, stream) for s in single]
+    ms_single = time_graphs(graphs, args.steps, args.warmup, stream)
+    del graphs, single
 
-    # per projection class: forward duration in a graph of back-to-back forwards
-    classes = {"attn 4096->4096 R205": "q_proj", "gate/up 4096->11008 R298": "gate_proj",
-               "down 11008->4096 R298": "down_proj"}
-    per_layer_count = {"attn 4096->4096 R205": 4, "gate/up 4096->11008 R298": 2, "down 11008->4096 R298": 1}
+    # per call kind: duration in a graph of back-to-back calls of that kind
     cls_stats = {}
-    for cname, name in classes.items():
-        K, N, ranks, us = forward_duration_us(gen, dev, name, stream)
-        b = proj_bytes(1, K, N, ranks)
-        cls_stats[cname] = {"us_per_forward": round(us, 3), "bytes": b, "gbs": b / us / 1e3,
-                            "share_us_per_layer": us * per_layer_count[cname]}
-    dom = max(cls_stats, key=lambda c: cls_stats[c]["share_us_per_layer"])
+    for kind, names in LAYER_CALLS:
+        call, us = call_duration_us(gen, dev, names, stream)
+        cls_stats[kind] = {"projections": "+".join(names), "us_per_call": round(us, 3), "bytes": call.bytes,
+                           "gbs": call.bytes / us / 1e3}
+    dom = max(cls_stats, key=lambda c: cls_stats[c]["us_per_call"])
     d = cls_stats[dom]
     roofline = {"bound": "hbm", "achieved": round(d["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": None,
-                "kernel": f"LittleBitLinear forward ({dom}): latent_mfma_kernel + expand_mfma_kernel",
-                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_forward"]}
+                "kernel": f"LittleBitLinear {dom} call ({d['projections']}): latent_mfma_kernel + expand_mfma_kernel",
+                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_call"]}
 
     cpu = None if args.no_cpu else cpu_baseline(args.layers, args.cpu_budget)
     value = step_bytes / (ms_cold * 1e-3) / 1e9
@@ -255,6 +280,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "llama2-7b-draft-0.1bpw-decode-step (224 LittleBitLinear forwards, M=1)",
+                   "launches": f"{2 * len(LAYER_CALLS)} per layer: q/k/v and gate/up as group calls",
                    "layers": args.layers, "hidden": 4096, "intermediate": 11008,
                    "ranks": {"attn": 205, "mlp": 298}, "batch": 1, "activations": "fp32",
                    "bytes_per_step": step_bytes, "weight_bytes_per_step": weight_bytes,
@@ -264,6 +290,8 @@ def main():
         "tok_per_s_linears": round(1000.0 / ms_cold, 2),
         "warm": {"ms_per_step": round(ms_warm, 4), "value": round(step_bytes / (ms_warm * 1e-3) / 1e9, 3),
                  "us_per_layer": round(ms_warm * 1000.0 / args.layers, 3)},
+        "ungrouped": {"ms_per_step": round(ms_single, 4), "value": round(step_bytes / (ms_single * 1e-3) / 1e9, 3),
+                      "launches": "14 per layer (each projection alone), cold"},
         "per_class": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in cls_stats.items()},
         "roofline": roofline,

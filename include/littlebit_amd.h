@@ -16,8 +16,13 @@
  *     pad bits 0 == +1); pass int32 or uint32 words, only the bits matter.
  *   - Return value 0 on success, a negative LBK_ERR_* code otherwise; the
  *     message of the last failure on the calling thread is lbk_last_error().
- *   - Stateless apart from the caller's workspace; calls on different streams
- *     must use different workspaces.
+ *   - Workspace: caller-owned device memory, zero-filled before its first
+ *     use and then kept for later calls (the library leaves its state there
+ *     in a form that any later call of any shape accepts).  One workspace
+ *     serves one stream; calls on different streams need different ones.
+ *     Calls can be captured in a HIP graph and replayed.
+ *   - Results of the MFMA path (M <= 16) are repeatable to about 1e-6
+ *     relative, not bit for bit: partial sums over K meet in fp32 atomics.
  */
 #ifndef LITTLEBIT_AMD_H
 #define LITTLEBIT_AMD_H
@@ -54,6 +59,18 @@ typedef struct lbk_branch {
   int64_t rank;          /* R >= 1                                          */
 } lbk_branch;
 
+/* One projection of a group call: its branches (1 or 2), out_features N,
+ * optional fp32 bias [N] and output y [M, N] (of the call's y_dtype). */
+typedef struct lbk_projection {
+  const lbk_branch* branches;
+  int n_branches;
+  int64_t out_features;
+  const float* bias;
+  void* y;
+} lbk_projection;
+
+#define LBK_MAX_GROUP 4
+
 /* ABI version (LBK_ABI_VERSION of the build). */
 int lbk_abi_version(void);
 
@@ -77,6 +94,21 @@ int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M,
                        int64_t K, int64_t N, const void* x, int x_dtype,
                        const float* bias, void* y, int y_dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace lbk_group_forward needs (0 with the error set if the
+ * shapes are invalid). */
+size_t lbk_group_workspace_bytes(const lbk_projection* projs, int n_proj,
+                                 int64_t M, int64_t K);
+
+/* Forward of up to LBK_MAX_GROUP projections that read the same x [M, K]
+ * (q/k/v of a decoder layer, or gate/up), in the launches of one
+ * projection: each y_p = lbk_linear_forward of projection p.  The sum of
+ * all branch ranks of the group is at most 16384.  Counterpart of the
+ * batched q/k/v and gate/up stages of the reference's CPU decode step
+ * (patches/littlebit_cpu_optimized.cpp:1700-1723, 1777-1798). */
+int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M,
+                      int64_t K, const void* x, int x_dtype, int y_dtype,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* One-branch form with the argument list of the reference operator
  * littlebit_cpu_ops::littlebit_linear (patches/littlebit_cpu_optimized.cpp:

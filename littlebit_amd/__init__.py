@@ -6,16 +6,20 @@ Public surface:
     ``littlebit_cpu_ops::littlebit_linear``
   * :class:`LittleBitProjection` / :class:`LittleBitBranch` -- prepared fused
     forward of a projection's draft and residual branches
+  * :class:`LittleBitProjectionGroup` -- projections sharing one input
+    (q/k/v, gate/up) in the launches of one
   * :func:`binary_packer` / :func:`binary_unpacker` -- the reference word format
 """
 from .binary_packer import binary_packer, binary_unpacker, words_per_row
-from .ops import LittleBitBranch, LittleBitProjection, littlebit_forward, littlebit_linear
+from .ops import (LittleBitBranch, LittleBitProjection, LittleBitProjectionGroup, littlebit_forward,
+                  littlebit_linear)
 from .modules import LittleBitLinear, sign_pm1
 
 __all__ = [
     "LittleBitLinear",
     "LittleBitBranch",
     "LittleBitProjection",
+    "LittleBitProjectionGroup",
     "littlebit_forward",
     "littlebit_linear",
     "binary_packer",

@@ -47,6 +47,20 @@ class LbkBranch(ctypes.Structure):
     ]
 
 
+class LbkProjection(ctypes.Structure):
+    """Mirror of ``lbk_projection``."""
+
+    _fields_ = [
+        ("branches", ctypes.POINTER(LbkBranch)),
+        ("n_branches", ctypes.c_int),
+        ("out_features", ctypes.c_int64),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+    ]
+
+
+LBK_MAX_GROUP = 4
+
 # name -> (restype, argtypes); must list every function of include/littlebit_amd.h
 _VP = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -58,6 +72,12 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(LbkBranch), ctypes.c_int, _I64, _I64, _I64, _VP, ctypes.c_int, _VP, _VP,
          ctypes.c_int, _VP, ctypes.c_size_t, _VP],
+    ),
+    "lbk_group_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LbkProjection), ctypes.c_int, _I64, _I64]),
+    "lbk_group_forward": (
+        ctypes.c_int,
+        [ctypes.POINTER(LbkProjection), ctypes.c_int, _I64, _I64, _VP, ctypes.c_int, ctypes.c_int, _VP,
+         ctypes.c_size_t, _VP],
     ),
     "lbk_littlebit_linear": (
         ctypes.c_int,

@@ -8,7 +8,8 @@
 // where sV and sU are +-1 read from words packed LSB first, bit 1 == -1
 // (quantization/utils/binary_packer.py:36-50).
 //
-// Two launches per projection, both branches in each.
+// Two launches per call, every branch in each; a call covers one projection
+// or a group of up to four projections that read the same x (q/k/v, gate/up).
 //
 // MFMA path (M <= 16):
 //   latent_mfma_kernel  grid = row-blocks (64 latent rows of one branch) x
@@ -16,15 +17,14 @@
 //                       g*x for its k-chunk to LDS (the MFMA A operand: rows
 //                       0-7 = hi of m 0-7, rows 8-15 = lo); each wave expands
 //                       its 16 rows' sign bytes into +-1 bf16 B operands in
-//                       registers and runs v_mfma_f32_16x16x32_bf16.  Partial
-//                       sums of the k-chunks go to workspace; the last block
-//                       of a row-block to arrive (a per-row-block counter that
-//                       it resets) adds them in fixed order, scales by l and
-//                       writes t.
-//   expand_mfma_kernel  grid = 64 output rows per block.  t of both branches
-//                       is staged in LDS as bf16 hi/lo; each wave expands the
-//                       U sign bytes of its 16 rows and accumulates both
-//                       branches, then writes h0*y0 + h1*y1 + bias.
+//                       registers and runs v_mfma_f32_16x16x32_bf16.  The
+//                       k-chunks add l-scaled partial sums into the latent
+//                       buffer t with fp32 atomics.
+//   expand_mfma_kernel  grid = 32 or 64 output rows of one projection per
+//                       block.  t of the projection's branches is staged in
+//                       LDS as bf16 hi/lo; each wave expands the U sign bytes
+//                       of its 16 rows and accumulates both branches, then
+//                       writes h0*y0 + h1*y1 + bias.
 // General path (any M): latent_valu_kernel / expand_valu_kernel, fp32 VALU.
 //
 // Splitting fp32 activations into bf16 hi + lo keeps the product error near
@@ -109,30 +109,47 @@ __device__ __forceinline__ void load8(const uint16_t* p, float (&a)[8]) {
 // MFMA path parameters
 // ---------------------------------------------------------------------------
 constexpr int kMaxWaveSteps = 24;  // sign-word steps per branch per expand wave
-// floats per latent half: M <= 16 rows of the padded ranks of both branches
-constexpr int kTHalf = kMaxMfmaM * (kMaxRankTotal + 2 * 128);
+constexpr int kMaxProj = 4;        // projections sharing one input in a group call
+constexpr int kMaxSeg = 2 * kMaxProj;
+// floats per latent half: M <= 16 rows of the padded ranks of every branch
+constexpr int kTHalf = kMaxMfmaM * (kMaxRankTotal + kMaxSeg * 128);
 
-struct MfmaParams {
-  const uint32_t* V[2];
-  const uint32_t* U[2];
-  const float* g[2];
-  const float* l[2];
-  const float* h[2];
-  int R[2];
+// Stage-1 operands of one branch ("segment") of a group call.
+struct LatSeg {
+  const uint32_t* V;  // [R, KW] sign words
+  const float* g;     // [K]
+  const float* l;     // [R]
+  int R;
+  int RP;     // padded latent row length (multiple of 128)
+  int rb0;    // first row-block of the segment
+  int tbase;  // offset of the segment's [M][RP] block in t
+};
+
+// Stage-2 operands of one projection (one or two segments) of a group call.
+struct ExpProj {
+  const uint32_t* U[2];  // [N, RW] sign words per branch
+  const float* h[2];     // [N]
+  const float* bias;     // [N] or null
+  void* y;               // [M, N]
   int RW[2];    // words per U row
   int RWp[2];   // RW rounded up to a multiple of 4
-  int rb0[2];   // first row-block of the branch
-  int RP[2];    // padded latent row length 32 * RWp (multiple of 128)
-  int tbase[2]; // offset of the branch's [M][RP] block in t
+  int RP[2];    // 32 * RWp
+  int tbase[2];
   int nb;
-  int M, K, KW, N;
-  int tsize;    // M * (RP[0] + RP[1]) floats
+  int N;
+  int tile0;    // first expand block of the projection
+};
+
+struct MfmaParams {
+  LatSeg seg[kMaxSeg];
+  ExpProj proj[kMaxProj];
+  int nseg, nproj;
+  int M, K, KW;
+  int tsize;    // M * sum(RP) floats
   int nkc;      // k-chunks
-  int xvec;     // x and v2 allow 16-byte loads (aligned, K % 8 == 0)
+  int xvec;     // x and every g allow 16-byte loads (aligned, K % 8 == 0)
   const void* x;
-  const float* bias;
-  void* y;
-  float* t2;       // two halves of kTHalf floats; per branch [M][RP] latent, l-scaled
+  float* t2;       // two halves of kTHalf floats; per segment [M][RP] latent, l-scaled
   uint32_t* sync;  // [0] P: half the next latent kernel accumulates into
                    // [1] Q: half the last latent kernel accumulated into
                    // [2 + h] floats of half h that may be non-zero
@@ -231,7 +248,7 @@ __device__ __forceinline__ void build_compact(u32x4* lds, int nch, int M, int ti
 
 // ---------------------------------------------------------------------------
 // Stage 1 (MFMA): t += l * (V_sign . (g*x)) over this block's k-chunk
-// grid.x = (row-blocks of all branches) * nkc, block = 256 threads (4 waves)
+// grid.x = (row-blocks of all segments) * nkc, block = 256 threads (4 waves)
 // LDS: compact A operand of g*x for the k-chunk (KC/8 chunks)
 //
 // The k-chunks of a row-block add into t with fp32 atomics (t is zero on
@@ -250,15 +267,20 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 
   const int rbk = int(blockIdx.x) / p.nkc;
   const int kc = int(blockIdx.x) - rbk * p.nkc;
-  // branch selection by value (no dynamic indexing of the kernel arguments)
-  const bool b1 = p.nb > 1 && rbk >= p.rb0[1];
-  const int rb = rbk - (b1 ? p.rb0[1] : 0);
-  const int R = b1 ? p.R[1] : p.R[0];
-  const int RP = b1 ? p.RP[1] : p.RP[0];
-  const int tbase = b1 ? p.tbase[1] : 0;
-  const float* __restrict__ g = b1 ? p.g[1] : p.g[0];
-  const float* __restrict__ lvec = b1 ? p.l[1] : p.l[0];
-  const uint32_t* __restrict__ V = b1 ? p.V[1] : p.V[0];
+  // segment of this row-block: a wave-uniform index, so the descriptor is
+  // read with scalar loads from the kernel arguments
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSeg; ++i) si += (i < p.nseg && rbk >= p.seg[i].rb0) ? 1 : 0;
+  si = __builtin_amdgcn_readfirstlane(si);
+  const LatSeg& SG = p.seg[si];
+  const int rb = rbk - SG.rb0;
+  const int R = SG.R;
+  const int RP = SG.RP;
+  const int tbase = SG.tbase;
+  const float* __restrict__ g = SG.g;
+  const float* __restrict__ lvec = SG.l;
+  const uint32_t* __restrict__ V = SG.V;
   const int k0 = kc * KC;
   const int tid = int(threadIdx.x);
   const int wave = tid / kWave;
@@ -364,12 +386,13 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b)
-// block = 2 * TILES waves covering 16 * TILES output rows: wave w owns tile
-// w % TILES (16 rows) and half w / TILES of the rank steps (4 sign words of
-// a row) of both branches; the two halves meet in LDS.  Every block reads
-// all of t, so larger M (a larger operand) takes more rows per block.
-// grid.x = ceil(N / (16 * TILES))
+// Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b) per projection
+// block = 2 * TILES waves covering 16 * TILES output rows of one projection:
+// wave w owns tile w % TILES (16 rows) and half w / TILES of the rank steps
+// (4 sign words of a row) of both branches; the two halves meet in LDS.
+// Every block reads all of its projection's t, so larger M (a larger
+// operand) takes more rows per block.
+// grid.x = sum over projections of ceil(N / (16 * TILES))
 // LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
 // ---------------------------------------------------------------------------
 template <int MT>
@@ -393,15 +416,20 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
   const int half = wave / E::TILES;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int n = int(blockIdx.x) * E::ROWS + tile * 16 + col;
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxProj; ++i) pi += (i < p.nproj && int(blockIdx.x) >= p.proj[i].tile0) ? 1 : 0;
+  pi = __builtin_amdgcn_readfirstlane(pi);
+  const ExpProj& P = p.proj[pi];
+  const int n = (int(blockIdx.x) - P.tile0) * E::ROWS + tile * 16 + col;
   // half of the latent buffer the latent kernel of this call filled; only
   // block 0 writes the state here, and only sync[0]
   const uint32_t hq = p.sync[1] & 1u;
-  const bool nvalid = n < p.N;
+  const bool nvalid = n < P.N;
 
   // this wave's steps: branch 0 steps [a0, a0 + n0), branch 1 steps [c0, c0 + n1)
-  const int steps0 = p.RWp[0] / 4;
-  const int steps = steps0 + (p.nb > 1 ? p.RWp[1] / 4 : 0);
+  const int steps0 = P.RWp[0] / 4;
+  const int steps = steps0 + (P.nb > 1 ? P.RWp[1] / 4 : 0);
   const int split = (steps + 1) / 2;
   const int q0 = half ? split : 0;
   const int q1 = half ? steps : split;
@@ -415,34 +443,35 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
   // waits on any of them.  Every element is written on every path.
   uint32_t pre0[S], pre1[S];
   {
-    const int RW0 = p.RW[0];
+    const int RW0 = P.RW[0];
     const int w0 = 4 * a0 + grp;
-    const uint32_t* __restrict__ u0 = p.U[0] + size_t(nvalid ? n : 0) * RW0 + w0;
+    const uint32_t* __restrict__ u0 = P.U[0] + size_t(nvalid ? n : 0) * RW0 + w0;
     const int lim0 = nvalid ? RW0 - w0 : 0;  // words of this lane left in the row
 #pragma unroll
     for (int i = 0; i < S; ++i) pre0[i] = (i < n0 && 4 * i < lim0) ? u0[4 * i] : 0u;
-    const int RW1 = p.nb > 1 ? p.RW[1] : 0;
+    const int RW1 = P.nb > 1 ? P.RW[1] : 0;
     const int w1 = 4 * c0 + grp;
-    const uint32_t* __restrict__ u1 = p.nb > 1 ? p.U[1] + size_t(nvalid ? n : 0) * RW1 + w1 : u0;
-    const int lim1 = (nvalid && p.nb > 1) ? RW1 - w1 : 0;
+    const uint32_t* __restrict__ u1 = P.nb > 1 ? P.U[1] + size_t(nvalid ? n : 0) * RW1 + w1 : u0;
+    const int lim1 = (nvalid && P.nb > 1) ? RW1 - w1 : 0;
 #pragma unroll
     for (int i = 0; i < S; ++i) pre1[i] = (i < n1 && 4 * i < lim1) ? u1[4 * i] : 0u;
   }
 
-  const int nch0 = 4 * p.RWp[0];
-  const int nch1 = p.nb > 1 ? 4 * p.RWp[1] : 0;
+  const int nch0 = 4 * P.RWp[0];
+  const int nch1 = P.nb > 1 ? 4 * P.RWp[1] : 0;
   u32x4* tb0 = lds_t;
   u32x4* tb1 = lds_t + size_t(L::MB) * nch0 * L::ROWS;
   {
     const int M = p.M;
     const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
-    const int RP0 = p.RP[0];
+    const float* __restrict__ t0 = ta + P.tbase[0];
+    const int RP0 = P.RP[0];
     build_compact<MT, E::THREADS>(tb0, nch0, M, tid, [&](int c, int m, float (&a)[8]) {
-      load8(ta + size_t(m) * RP0 + 8 * c, a);
+      load8(t0 + size_t(m) * RP0 + 8 * c, a);
     });
-    if (p.nb > 1) {
-      const float* __restrict__ t1 = ta + p.tbase[1];
-      const int RP1 = p.RP[1];
+    if (P.nb > 1) {
+      const float* __restrict__ t1 = ta + P.tbase[1];
+      const int RP1 = P.RP[1];
       build_compact<MT, E::THREADS>(tb1, nch1, M, tid, [&](int c, int m, float (&a)[8]) {
         load8(t1 + size_t(m) * RP1 + 8 * c, a);
       });
@@ -489,8 +518,8 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
   }
 
   // h-weighted branch sum of this half; C rows 4*grp + i (grp 0,1 hi, 2,3 lo)
-  const float h0 = nvalid ? p.h[0][n] : 0.f;
-  const float h1 = (nvalid && p.nb > 1) ? p.h[1][n] : 0.f;
+  const float h0 = nvalid ? P.h[0][n] : 0.f;
+  const float h1 = (nvalid && P.nb > 1) ? P.h[1][n] : 0.f;
   float out[L::MB][4];
 #pragma unroll
   for (int mb = 0; mb < L::MB; ++mb)
@@ -507,14 +536,15 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
   }
   __syncthreads();
   if (half == 0 && lane < 32 && nvalid) {
-    const float bn = p.bias ? p.bias[n] : 0.f;
-    YT* y = static_cast<YT*>(p.y);
+    const float bn = P.bias ? P.bias[n] : 0.f;
+    YT* y = static_cast<YT*>(P.y);
+    const int N = P.N;
 #pragma unroll
     for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = mb * 8 + grp * 4 + i;
-        if (m < p.M) store_out(y, size_t(m) * p.N + n, out[mb][i] + red[tile][mb * 4 + i][lane] + bn);
+        if (m < p.M) store_out(y, size_t(m) * N + n, out[mb][i] + red[tile][mb * 4 + i][lane] + bn);
       }
   }
 
@@ -713,22 +743,39 @@ int check_launch(const char* what) {
   return LBK_OK;
 }
 
-int validate(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N) {
-  if (!branches) return set_error(LBK_ERR_ARG, "branches is NULL");
-  if (n_branches < 1 || n_branches > 2) return set_error(LBK_ERR_ARG, "n_branches must be 1 or 2, got %d", n_branches);
+// One projection of a group call as the host sees it.
+struct ProjDesc {
+  const lbk_branch* br;
+  int nb;
+  int64_t N;
+  const float* bias;
+  void* y;
+};
+
+int validate_group(const ProjDesc* pd, int np, int64_t M, int64_t K) {
+  if (np < 1 || np > kMaxProj) return set_error(LBK_ERR_ARG, "n_proj must be in [1, %d], got %d", kMaxProj, np);
   if (M < 0 || M > kMaxDim)
     return set_error(LBK_ERR_ARG, "M must be in [0, %lld], got %lld", (long long)kMaxDim, (long long)M);
   if (K < 1 || K > kMaxDim)
     return set_error(LBK_ERR_ARG, "K must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)K);
-  if (N < 1 || N > kMaxDim)
-    return set_error(LBK_ERR_ARG, "N must be in [1, %lld], got %lld", (long long)kMaxDim, (long long)N);
   int64_t rsum = 0;
-  for (int b = 0; b < n_branches; ++b) {
-    const lbk_branch& B = branches[b];
-    if (B.rank < 1) return set_error(LBK_ERR_ARG, "branch %d: rank must be >= 1, got %lld", b, (long long)B.rank);
-    if (!B.v_sign || !B.u_sign || !B.v2 || !B.mid || !B.u1)
-      return set_error(LBK_ERR_ARG, "branch %d: NULL factor or scale pointer", b);
-    rsum += B.rank;
+  for (int q = 0; q < np; ++q) {
+    const ProjDesc& P = pd[q];
+    if (!P.br) return set_error(LBK_ERR_ARG, "projection %d: branches is NULL", q);
+    if (P.nb < 1 || P.nb > 2)
+      return set_error(LBK_ERR_ARG, "projection %d: n_branches must be 1 or 2, got %d", q, P.nb);
+    if (P.N < 1 || P.N > kMaxDim)
+      return set_error(LBK_ERR_ARG, "projection %d: N must be in [1, %lld], got %lld", q, (long long)kMaxDim,
+                       (long long)P.N);
+    for (int b = 0; b < P.nb; ++b) {
+      const lbk_branch& B = P.br[b];
+      if (B.rank < 1)
+        return set_error(LBK_ERR_ARG, "projection %d branch %d: rank must be >= 1, got %lld", q, b,
+                         (long long)B.rank);
+      if (!B.v_sign || !B.u_sign || !B.v2 || !B.mid || !B.u1)
+        return set_error(LBK_ERR_ARG, "projection %d branch %d: NULL factor or scale pointer", q, b);
+      rsum += B.rank;
+    }
   }
   if (rsum > kMaxRankTotal)
     return set_error(LBK_ERR_ARG, "sum of branch ranks %lld exceeds %lld", (long long)rsum, (long long)kMaxRankTotal);
@@ -737,8 +784,8 @@ int validate(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, i
 
 // Workspace layout (byte offsets), fixed so that calls of any shape on one
 // workspace keep its invariants:
-//   [0, kCounterBytes)                 counters, zero between calls
-//   [kTOffset, kTOffset + kTBytes)     MFMA-path latent halves (see MfmaParams)
+//   [0, kCounterBytes)                 latent-buffer state (see MfmaParams)
+//   [kTOffset, kTOffset + kTBytes)     MFMA-path latent halves
 //   [kValuOffset, ...)                 general-path latent buffers
 constexpr size_t kTOffset = 4096;
 constexpr size_t kTBytes = 2 * size_t(kTHalf) * sizeof(float);
@@ -751,7 +798,7 @@ struct Plan {
   int mt;        // M tile of the MFMA path: 1, 2, 4, 8 or 16
   int wpl;       // words per lane in latent_mfma_kernel
   int nkc;       // k-chunks
-  int nrb;       // row-blocks over all branches
+  int nrb;       // row-blocks over all segments
   int wsteps;    // expand_mfma_kernel unroll bound S
   size_t lds1, lds2;
   size_t ws_total;
@@ -765,18 +812,28 @@ size_t compact_rows(int mt, int64_t nch) {
   return size_t(mb) * size_t(nch) * size_t(2 * mr + 1);
 }
 
-Plan make_plan(const lbk_branch* br, int nb, int64_t M, int64_t K) {
+Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   Plan pl{};
-  int64_t rwp_sum = 0, nrb = 0;
-  for (int b = 0; b < nb; ++b) {
-    rwp_sum += ceil_div(ceil_div(br[b].rank, 32), 4) * 4;
-    nrb += ceil_div(br[b].rank, kRowBlock);
+  int64_t nrb = 0, steps_max = 0;
+  size_t lds2 = 0, valu_bytes = 0;
+  pl.mt = mtile(M);
+  for (int q = 0; q < np; ++q) {
+    int64_t rwp_sum = 0;
+    size_t vb = 0;
+    for (int b = 0; b < pd[q].nb; ++b) {
+      const int64_t R = pd[q].br[b].rank;
+      rwp_sum += ceil_div(ceil_div(R, 32), 4) * 4;
+      nrb += ceil_div(R, kRowBlock);
+      vb += align256(size_t(M) * size_t(R) * sizeof(float));
+    }
+    const size_t l2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
+    if (l2 > lds2) lds2 = l2;
+    const int64_t ws = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
+    if (ws > steps_max) steps_max = ws;
+    if (vb > valu_bytes) valu_bytes = vb;
   }
   pl.nrb = int(nrb);
-  pl.mt = mtile(M);
-  const size_t lds2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
-  const int64_t wave_steps = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
-  pl.mfma = (M >= 1 && M <= kMaxMfmaM && lds2 <= size_t(kMaxLds) && wave_steps <= kMaxWaveSteps);
+  pl.mfma = (M >= 1 && M <= kMaxMfmaM && lds2 <= size_t(kMaxLds) && steps_max <= kMaxWaveSteps);
   if (pl.mfma) {
     // enough blocks to cover the CUs, short per-wave chains
     pl.wpl = 2;
@@ -784,14 +841,12 @@ Plan make_plan(const lbk_branch* br, int nb, int64_t M, int64_t K) {
       if (nrb * ceil_div(K, 128 * w) >= 256) { pl.wpl = w; break; }
     }
     pl.nkc = int(ceil_div(K, 128 * pl.wpl));
-    pl.wsteps = wave_steps <= 4 ? 4 : wave_steps <= 8 ? 8 : wave_steps <= 16 ? 16 : 24;
+    pl.wsteps = steps_max <= 4 ? 4 : steps_max <= 8 ? 8 : steps_max <= 16 ? 16 : 24;
     pl.lds1 = compact_rows(pl.mt, 128 * pl.wpl / 8) * 16;
     pl.lds2 = lds2;
     pl.ws_total = kTOffset + kTBytes;
   } else {
-    size_t bytes = kValuOffset;
-    for (int b = 0; b < nb; ++b) bytes += align256(size_t(M) * size_t(br[b].rank) * sizeof(float));
-    pl.ws_total = bytes;
+    pl.ws_total = kValuOffset + valu_bytes;
   }
   return pl;
 }
@@ -822,9 +877,8 @@ void dispatch_latent(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
 }
 
 template <typename YT, int MT, int S>
-void launch_expand_mfma_s(const MfmaParams& p, int /*unused*/, size_t lds, hipStream_t s) {
+void launch_expand_mfma_s(const MfmaParams& p, int grid, size_t lds, hipStream_t s) {
   using E = ExpandShape<MT>;
-  const int grid = int(ceil_div(p.N, E::ROWS));
   hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S>), dim3(grid), dim3(E::THREADS), lds, s, p);
 }
 
@@ -849,40 +903,54 @@ void dispatch_expand(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
   }
 }
 
-int forward_mfma(const lbk_branch* branches, int nb, const Plan& pl, int64_t M, int64_t K, int64_t N,
-                 const void* x, int x_dtype, const float* bias, void* y, int y_dtype, void* workspace,
-                 hipStream_t s) {
+int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
+                 int y_dtype, void* workspace, hipStream_t s) {
+  using E1 = ExpandShape<1>;
+  using E4 = ExpandShape<4>;
+  const int rows = pl.mt >= 4 ? E4::ROWS : E1::ROWS;
   MfmaParams p;
   memset(&p, 0, sizeof(p));
-  p.nb = nb;
+  p.nproj = np;
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
-  p.N = int(N);
-  int rb = 0, tbase = 0;
-  for (int b = 0; b < nb; ++b) {
-    const lbk_branch& S = branches[b];
-    p.V[b] = reinterpret_cast<const uint32_t*>(S.v_sign);
-    p.U[b] = reinterpret_cast<const uint32_t*>(S.u_sign);
-    p.g[b] = S.v2;
-    p.l[b] = S.mid;
-    p.h[b] = S.u1;
-    p.R[b] = int(S.rank);
-    p.RW[b] = int(ceil_div(S.rank, 32));
-    p.RWp[b] = int(ceil_div(p.RW[b], 4) * 4);
-    p.rb0[b] = rb;
-    p.RP[b] = 32 * p.RWp[b];
-    p.tbase[b] = tbase;
-    rb += int(ceil_div(S.rank, kRowBlock));
-    tbase += int(M) * p.RP[b];
+  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  int rb = 0, tbase = 0, si = 0, tile = 0;
+  for (int q = 0; q < np; ++q) {
+    ExpProj& P = p.proj[q];
+    P.nb = pd[q].nb;
+    P.N = int(pd[q].N);
+    P.bias = pd[q].bias;
+    P.y = pd[q].y;
+    P.tile0 = tile;
+    tile += int(ceil_div(pd[q].N, rows));
+    for (int b = 0; b < pd[q].nb; ++b, ++si) {
+      const lbk_branch& B = pd[q].br[b];
+      LatSeg& S = p.seg[si];
+      S.V = reinterpret_cast<const uint32_t*>(B.v_sign);
+      S.g = B.v2;
+      S.l = B.mid;
+      S.R = int(B.rank);
+      const int RW = int(ceil_div(B.rank, 32));
+      const int RWp = int(ceil_div(RW, 4) * 4);
+      S.RP = 32 * RWp;
+      S.rb0 = rb;
+      S.tbase = tbase;
+      P.U[b] = reinterpret_cast<const uint32_t*>(B.u_sign);
+      P.h[b] = B.u1;
+      P.RW[b] = RW;
+      P.RWp[b] = RWp;
+      P.RP[b] = S.RP;
+      P.tbase[b] = tbase;
+      rb += int(ceil_div(B.rank, kRowBlock));
+      tbase += int(M) * S.RP;
+      xvec = xvec && (reinterpret_cast<uintptr_t>(B.v2) % 16) == 0;
+    }
   }
+  p.nseg = si;
   p.tsize = tbase;
   p.nkc = pl.nkc;
   p.x = x;
-  p.bias = bias;
-  p.y = y;
-  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
-  for (int b = 0; b < nb; ++b) xvec = xvec && (reinterpret_cast<uintptr_t>(branches[b].v2) % 16) == 0;
   p.xvec = xvec ? 1 : 0;
   char* ws = static_cast<char*>(workspace);
   p.sync = reinterpret_cast<uint32_t*>(ws);
@@ -894,8 +962,8 @@ int forward_mfma(const lbk_branch* branches, int nb, const Plan& pl, int64_t M, 
   int rc = check_launch("latent_mfma_kernel");
   if (rc != LBK_OK) return rc;
 
-  if (y_dtype == LBK_F32) dispatch_expand<float>(p, pl, 0, s);
-  else dispatch_expand<uint16_t>(p, pl, 0, s);
+  if (y_dtype == LBK_F32) dispatch_expand<float>(p, pl, tile, s);
+  else dispatch_expand<uint16_t>(p, pl, tile, s);
   return check_launch("expand_mfma_kernel");
 }
 
@@ -988,6 +1056,28 @@ int forward_valu(const lbk_branch* branches, int nb, int64_t M, int64_t K, int64
   return check_launch("expand_valu_kernel");
 }
 
+int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, int y_dtype,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_group(pd, np, M, K);
+  if (rc != LBK_OK) return rc;
+  if (x_dtype != LBK_F32 && x_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "x_dtype %d unsupported", x_dtype);
+  if (y_dtype != LBK_F32 && y_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "y_dtype %d unsupported", y_dtype);
+  if (M == 0) return LBK_OK;
+  if (!x) return set_error(LBK_ERR_ARG, "x is NULL");
+  for (int q = 0; q < np; ++q)
+    if (!pd[q].y) return set_error(LBK_ERR_ARG, "projection %d: y is NULL", q);
+  const Plan pl = make_plan(pd, np, M, K);
+  if (!workspace || workspace_bytes < pl.ws_total)
+    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.mfma) return forward_mfma(pd, np, pl, M, K, x, x_dtype, y_dtype, workspace, s);
+  for (int q = 0; q < np; ++q) {
+    rc = forward_valu(pd[q].br, pd[q].nb, M, K, pd[q].N, x, x_dtype, pd[q].bias, pd[q].y, y_dtype, workspace, s);
+    if (rc != LBK_OK) return rc;
+  }
+  return LBK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -996,28 +1086,41 @@ int lbk_abi_version(void) { return LBK_ABI_VERSION; }
 
 const char* lbk_last_error(void) { return g_last_error; }
 
+size_t lbk_group_workspace_bytes(const lbk_projection* projs, int n_proj, int64_t M, int64_t K) {
+  ProjDesc pd[kMaxProj];
+  if (!projs || n_proj < 1 || n_proj > kMaxProj) {
+    set_error(LBK_ERR_ARG, "n_proj must be in [1, %d] with a non-NULL array, got %d", kMaxProj, n_proj);
+    return 0;
+  }
+  for (int q = 0; q < n_proj; ++q)
+    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y};
+  if (validate_group(pd, n_proj, M, K) != LBK_OK) return 0;
+  return make_plan(pd, n_proj, M, K).ws_total;
+}
+
+int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x, int x_dtype,
+                      int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  if (!projs || n_proj < 1 || n_proj > kMaxProj)
+    return set_error(LBK_ERR_ARG, "n_proj must be in [1, %d] with a non-NULL array, got %d", kMaxProj, n_proj);
+  ProjDesc pd[kMaxProj];
+  for (int q = 0; q < n_proj; ++q)
+    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y};
+  return forward_group(pd, n_proj, M, K, x, x_dtype, y_dtype, workspace, workspace_bytes, stream);
+}
+
 size_t lbk_linear_workspace_bytes(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N) {
-  if (validate(branches, n_branches, M, K, N) != LBK_OK) return 0;
-  return make_plan(branches, n_branches, M, K).ws_total;
+  const ProjDesc pd{branches, n_branches, N, nullptr, nullptr};
+  if (validate_group(&pd, 1, M, K) != LBK_OK) return 0;
+  return make_plan(&pd, 1, M, K).ws_total;
 }
 
 int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N,
                        const void* x, int x_dtype, const float* bias, void* y, int y_dtype, void* workspace,
                        size_t workspace_bytes, void* stream) {
   g_last_error[0] = '\0';
-  int rc = validate(branches, n_branches, M, K, N);
-  if (rc != LBK_OK) return rc;
-  if (x_dtype != LBK_F32 && x_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "x_dtype %d unsupported", x_dtype);
-  if (y_dtype != LBK_F32 && y_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "y_dtype %d unsupported", y_dtype);
-  if (M == 0) return LBK_OK;
-  if (!x || !y) return set_error(LBK_ERR_ARG, "x or y is NULL");
-  const Plan pl = make_plan(branches, n_branches, M, K);
-  if (!workspace || workspace_bytes < pl.ws_total)
-    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.mfma)
-    return forward_mfma(branches, n_branches, pl, M, K, N, x, x_dtype, bias, y, y_dtype, workspace, s);
-  return forward_valu(branches, n_branches, M, K, N, x, x_dtype, bias, y, y_dtype, workspace, s);
+  const ProjDesc pd{branches, n_branches, N, bias, y};
+  return forward_group(&pd, 1, M, K, x, x_dtype, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const int32_t* v_sign, int64_t v_cols,

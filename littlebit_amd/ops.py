@@ -8,6 +8,10 @@
 * :class:`LittleBitBranch` / :class:`LittleBitProjection` hold one
   projection's device-resident packed factors and scales and run the fused
   forward (all branches + bias in one call) through ``lbk_linear_forward``.
+* :class:`LittleBitProjectionGroup` runs up to four projections that read the
+  same input (q/k/v, gate/up) in the launches of one, through
+  ``lbk_group_forward`` -- the GPU form of the reference decode step's
+  batched q/k/v and gate/up stages (patch:1697-1723, 1777-1798).
 
 Everything here requires CUDA (HIP) tensors; there is no CPU path.
 """
@@ -24,6 +28,7 @@ from . import _lib
 __all__ = [
     "LittleBitBranch",
     "LittleBitProjection",
+    "LittleBitProjectionGroup",
     "littlebit_linear",
     "littlebit_forward",
     "workspace_for",
@@ -185,6 +190,73 @@ class LittleBitProjection:
             out.data_ptr(), _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "lbk_linear_forward")
         return out
+
+    __call__ = forward
+
+
+class LittleBitProjectionGroup:
+    """Projections that read the same input, run together.
+
+    ``forward(x)`` returns ``[p.forward(x) for p in projections]`` (same
+    values, to the MFMA path's run-to-run tolerance) from two launches in
+    total instead of two per projection."""
+
+    def __init__(self, projections: Sequence[LittleBitProjection]):
+        _check(1 <= len(projections) <= _lib.LBK_MAX_GROUP,
+               f"a group has 1 to {_lib.LBK_MAX_GROUP} projections, got {len(projections)}")
+        self.projections = list(projections)
+        self.in_features = self.projections[0].in_features
+        self.device = self.projections[0].device
+        for i, p in enumerate(self.projections):
+            _check(p.in_features == self.in_features, f"projection {i}: in_features differs within the group")
+            _check(p.device == self.device, f"projection {i}: all projections must be on one device")
+        arr = (_lib.LbkProjection * len(self.projections))()
+        for i, p in enumerate(self.projections):
+            arr[i].branches = ctypes.cast(p._arr, ctypes.POINTER(_lib.LbkBranch))
+            arr[i].n_branches = len(p.branches)
+            arr[i].out_features = p.out_features
+            arr[i].bias = p.bias.data_ptr() if p.bias is not None else None
+        self._arr = arr
+
+    def workspace_bytes(self, M: int) -> int:
+        lib = _lib.load()
+        n = lib.lbk_group_workspace_bytes(self._arr, len(self.projections), int(M), self.in_features)
+        if n == 0 and M > 0:
+            _lib.check(_lib.LBK_ERR_ARG, "lbk_group_workspace_bytes")
+        return int(n)
+
+    def forward(self, x: torch.Tensor, outs: Optional[Sequence[torch.Tensor]] = None,
+                out_dtype: Optional[torch.dtype] = None) -> list:
+        _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
+        _check(x.device == self.device, "input must be on the factors' device")
+        _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
+        _check(x.shape[-1] == self.in_features,
+               f"input last dimension {x.shape[-1]} != in_features {self.in_features}")
+        lead = tuple(x.shape[:-1])
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        M = x2.shape[0]
+        odt = out_dtype or x.dtype
+        _check(odt in _DTYPE_CODES, f"output dtype {odt} unsupported")
+        if outs is None:
+            outs = [torch.empty((*lead, p.out_features), dtype=odt, device=x.device) for p in self.projections]
+        else:
+            _check(len(outs) == len(self.projections), "one output per projection")
+            for o, p in zip(outs, self.projections):
+                _check(o.is_cuda and o.is_contiguous() and o.dtype == odt and o.numel() == M * p.out_features,
+                       "an output has the wrong shape, dtype or layout")
+        if M == 0:
+            return list(outs)
+        for i, o in enumerate(outs):
+            self._arr[i].y = o.data_ptr()
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        ws = workspace_for(x.device, stream, self.workspace_bytes(M))
+        rc = lib.lbk_group_forward(self._arr, len(self.projections), M, self.in_features, x2.data_ptr(),
+                                   _DTYPE_CODES[x.dtype], _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "lbk_group_forward")
+        return list(outs)
 
     __call__ = forward
 

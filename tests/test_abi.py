@@ -103,6 +103,61 @@ def test_workspace_query():
     assert lib.lbk_linear_workspace_bytes(br, 5, 8, 4096, 4096) == 0
 
 
+def _group(n, rank=8, N=64):
+    import littlebit_amd._lib as L
+    brs = [_branch(rank) for _ in range(n)]
+    arr = (L.LbkProjection * max(n, 1))()
+    for i in range(n):
+        arr[i].branches = ctypes.cast(brs[i], ctypes.POINTER(L.LbkBranch))
+        arr[i].n_branches = 2
+        arr[i].out_features = N
+        arr[i].y = 0x1000
+    return arr, brs
+
+
+def test_group_struct_layout():
+    import littlebit_amd._lib as L
+    assert ctypes.sizeof(L.LbkProjection) == 40
+    assert L.LbkProjection.out_features.offset == 16 and L.LbkProjection.y.offset == 32
+
+
+def test_group_validation_errors():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    arr, keep = _group(4)
+    fwd = lib.lbk_group_forward
+    assert fwd(arr, 0, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "n_proj" in L.last_error()
+    assert fwd(arr, 5, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    arr[2].y = None
+    assert fwd(arr, 4, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "projection 2" in L.last_error()
+    arr[2].y = 0x1000
+    arr[1].n_branches = 3
+    assert fwd(arr, 4, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "projection 1" in L.last_error()
+    arr[1].n_branches = 2
+    assert fwd(arr, 4, 1, 64, 0x1000, 9, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_DTYPE
+    assert fwd(arr, 4, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 16, None) == L.LBK_ERR_WORKSPACE
+    # total rank over the group is bounded
+    big, keep2 = _group(3, rank=3000)
+    assert fwd(big, 3, 1, 64, 0x1000, L.LBK_F32, L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "ranks" in L.last_error()
+    assert fwd(arr, 4, 0, 64, None, L.LBK_F32, L.LBK_F32, None, 0, None) == L.LBK_OK
+
+
+def test_group_workspace_query():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    arr, keep = _group(3, rank=205, N=4096)
+    br = _branch(rank=205)
+    one = lib.lbk_linear_workspace_bytes(br, 2, 8, 4096, 4096)
+    grp = lib.lbk_group_workspace_bytes(arr, 3, 8, 4096)
+    assert 0 < one <= grp
+    assert lib.lbk_group_workspace_bytes(arr, 3, 64, 4096) > grp  # general path: per-call latent buffers
+    assert lib.lbk_group_workspace_bytes(arr, 0, 8, 4096) == 0
+
+
 def test_pack_unpack_argument_errors():
     import littlebit_amd._lib as L
     lib = L.load()

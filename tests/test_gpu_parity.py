@@ -217,6 +217,109 @@ def test_graph_replay_matches_eager(gpu):
         torch.cuda.synchronize()
 
 
+# --------------------------------------------------------------------------- projection groups
+def _run_group(dev, x, projs, x_dtype=torch.float32, out_dtype=None):
+    """projs: list of (branches, bias or None); one lbk_group_forward call."""
+    from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+    group = LittleBitProjectionGroup([
+        LittleBitProjection([_dev_branch(b, dev) for b in brs], None if bias is None else torch.from_numpy(bias).to(dev))
+        for brs, bias in projs])
+    tx = torch.from_numpy(np.asarray(x, np.float32)).to(dev).to(x_dtype)
+    ys = group.forward(tx, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return [y.float().cpu().numpy() for y in ys], tx.float().cpu().numpy()
+
+
+def _group_case(seed, M, K, specs, bias=False):
+    """specs: [(N, ranks)]; x shared, each projection its own seeded factors."""
+    from littlebit_amd.synthetic import make_projection
+    x = None
+    projs = []
+    for i, (N, ranks) in enumerate(specs):
+        xi, brs = make_projection(seed + 17 * i, M, K, N, ranks)
+        x = xi if x is None else x
+        b = (np.random.Generator(np.random.PCG64(seed + i)).standard_normal(N).astype(np.float32)
+             if bias else None)
+        projs.append(([br.as_dict() for br in brs], b))
+    return x, projs
+
+
+@pytest.mark.parametrize("what,M,K,specs", [
+    ("qkv draft", 1, 4096, [(4096, [205])] * 3),
+    ("qkv target", 8, 4096, [(4096, [205, 1843])] * 3),
+    ("gate/up target", 8, 4096, [(11008, [298, 2686])] * 2),
+    ("gate/up draft", 1, 4096, [(11008, [298])] * 2),
+    ("llama3 q/k/v gqa", 4, 4096, [(4096, [204, 1843]), (1024, [81, 737]), (1024, [81, 737])]),
+    ("ragged four", 3, 70, [(45, [37]), (77, [64, 95]), (31, [31, 1]), (5, [3])]),
+    ("tree M=16", 16, 4096, [(4096, [205, 1843])] * 3),
+    ("general path M=20", 20, 4096, [(4096, [205]), (1024, [81, 9])]),
+])
+def test_group_matches_oracle(gpu, what, M, K, specs):
+    x, projs = _group_case(3000 + M, M, K, specs)
+    ys, xu = _run_group(gpu, x, projs)
+    for i, ((brs, _), y) in enumerate(zip(projs, ys)):
+        _check(y, xu, brs, K, specs[i][0], TOL_F32, what=f"{what} proj {i}")
+
+
+def test_group_bias_bf16(gpu):
+    K = 512
+    specs = [(300, [45, 301]), (512, [64])]
+    x, projs = _group_case(3100, 2, K, specs, bias=True)
+    ys, xu = _run_group(gpu, x, projs, x_dtype=torch.bfloat16, out_dtype=torch.bfloat16)
+    for i, ((brs, b), y) in enumerate(zip(projs, ys)):
+        _check(y, xu, brs, K, specs[i][0], TOL_BF16_OUT, bias=b, what=f"bias bf16 proj {i}")
+
+
+def test_group_equals_single_calls(gpu):
+    """A group's outputs equal the projections' separate forwards."""
+    from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+    K = 4096
+    x, projs = _group_case(3200, 8, K, [(4096, [205, 1843]), (4096, [205]), (1024, [81])])
+    ps = [LittleBitProjection([_dev_branch(b, gpu) for b in brs]) for brs, _ in projs]
+    tx = torch.from_numpy(x).to(gpu)
+    ys = LittleBitProjectionGroup(ps).forward(tx)
+    for i, p in enumerate(ps):
+        y1 = p.forward(tx)
+        torch.cuda.synchronize()
+        assert O.rel_err(ys[i].cpu().numpy(), y1.cpu().numpy()) <= 1e-5, f"proj {i}"
+
+
+def test_group_graph_replay_interleaved(gpu):
+    """Groups and single projections captured in one graph, replayed with
+    eager work in between; every replay matches the eager outputs."""
+    from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+    K = 4096
+    x, projs = _group_case(3300, 1, K, [(4096, [205])] * 3)
+    ps = [LittleBitProjection([_dev_branch(b, gpu) for b in brs]) for brs, _ in projs]
+    grp = LittleBitProjectionGroup(ps)
+    tx = torch.from_numpy(x).to(gpu)
+    outs = [torch.empty((1, 4096), device=gpu) for _ in range(3)]
+    single = torch.empty((1, 4096), device=gpu)
+
+    def step():
+        grp.forward(tx, outs=outs)
+        ps[0].forward(outs[2], out=single)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    s.synchronize()
+    eager = [o.clone() for o in outs] + [single.clone()]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    for rep in range(4):
+        for o in outs + [single]:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs + [single], eager)):
+            assert O.rel_err(o.cpu().numpy(), e.cpu().numpy()) <= 1e-5, f"replay {rep} output {i}"
+        ps[1].forward(tx)  # eager call on another stream's workspace in between
+        torch.cuda.synchronize()
+
+
 # --------------------------------------------------------------------------- module / op boundary
 def test_module_forward_matches_oracle(gpu):
     from littlebit_amd import LittleBitLinear
