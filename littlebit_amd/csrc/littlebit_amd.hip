@@ -25,7 +25,8 @@
 //                       LDS as bf16 hi/lo; each wave expands the U sign bytes
 //                       of its 16 rows and accumulates both branches, then
 //                       writes h0*y0 + h1*y1 + bias.
-// General path (any M): latent_valu_kernel / expand_valu_kernel, fp32 VALU.
+// GEMM path (M > 16, or operands too large for the decode path's LDS):
+//   gemm_latent_kernel / gemm_expand_kernel, tiled on v_mfma_f32_32x32x16_bf16.
 //
 // Splitting fp32 activations into bf16 hi + lo keeps the product error near
 // 2^-17 relative: +-1 is exact in bf16 and the MFMA accumulates in fp32.
@@ -35,6 +36,8 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
+
+#include <type_traits>
 
 #include "littlebit_amd.h"
 
@@ -52,10 +55,8 @@ int set_error(int code, const char* fmt, ...) {
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;
-constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int64_t kMaxDim = int64_t(1) << 24;  // K, N, M limit
 constexpr int64_t kMaxRankTotal = 16384;       // sum of branch ranks
-constexpr int kValuLdsBudget = 64 * 1024;      // t staging in expand_valu_kernel
 constexpr int kMaxLds = 159 * 1024;            // gfx950: 160 KB per workgroup, 1 KB kept for static LDS
 constexpr int kRowBlock = 64;                  // latent rows per latent_mfma block
 constexpr int kMaxMfmaM = 16;                  // MFMA path handles M <= 16
@@ -555,150 +556,272 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
 }
 
 // ---------------------------------------------------------------------------
-// General path (fp32 VALU, any M)
+// GEMM path (M > 16, and shapes the decode path cannot stage in LDS): a
+// tiled sign-GEMM on v_mfma_f32_32x32x16_bf16.
+//   stage 1  T[m, r] = l[r] * sum_k sV[r, k] * g[k] * x[m, k]
+//   stage 2  y[m, n] = bias[n] + sum_b h_b[n] * sum_r sU_b[n, r] * T_b[m, r]
+// Block tile 128 (m) x 128 (columns: latent rows in stage 1, outputs in
+// stage 2), 4 waves of 64 x 64 (2 x 2 MFMA tiles), k-steps of 32.  The A
+// tile (activations) is staged in LDS as bf16, double-buffered; the +-1 B
+// operand is expanded in registers from the sign word of the lane's column:
+// for sub-step s of a k-step, lane l (column l % 32, k 8*(l/32) .. +8 of
+// the 32x32x16 operand) takes byte 2*s + l/32 of that word.
+// SPLIT (fp32 activations): A is staged as bf16 hi and lo tiles, both go
+// through the MFMA, so products keep ~2^-17 relative error; T is fp32.
+// Without SPLIT (bf16 activations): A = bf16(g*x) and T is bf16, the
+// precision of the reference's bf16 forward (littlebit.py:116-121).
 // ---------------------------------------------------------------------------
-struct DevBranch {
-  const uint32_t* v;  // [R, KW]
-  const uint32_t* u;  // [N, RW]
+constexpr int kGB = 128;             // block tile (m and columns)
+constexpr int kGK = 32;              // k per step
+constexpr int kGThreads = 256;
+constexpr int kGRow = 40;            // bf16 per LDS row: 32 + 8 pad (80 B rows, 16-byte aligned)
+constexpr int kGTile = kGB * kGRow;  // bf16 per LDS tile
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct GemmSeg {      // stage-1 operands of one branch
+  const uint32_t* V;  // [R, KW]
   const float* g;     // [K]
   const float* l;     // [R]
-  const float* h;     // [N]
-  float* t;           // workspace [M, R], l-scaled latent
   int R;
-  int RW;
-  int block0;         // first latent_valu_kernel block of this branch
+  int RP;             // T row length: R rounded up to kGB
+  int nt0;            // first column tile of the segment
+  int64_t tbase;      // element offset of the segment's [M][RP] block of T
 };
 
-struct ValuParams {
-  DevBranch br[2];
-  int nb;
-  int M, K, KW, N;
-  const void* x;
+struct GemmProj {     // stage-2 operands of one projection
+  const uint32_t* U[2];
+  const float* h[2];
   const float* bias;
   void* y;
+  int RW[2];          // words per U row = k-steps of stage 2
+  int RP[2];
+  int64_t tbase[2];
+  int nb;
+  int N;
+  int nt0;            // first column tile of the projection
 };
 
-__device__ __forceinline__ DevBranch pick(const ValuParams& p, int b) { return b ? p.br[1] : p.br[0]; }
+struct GemmParams {
+  GemmSeg seg[kMaxSeg];
+  GemmProj proj[kMaxProj];
+  int nseg, nproj;
+  int M, K, KW;
+  int xvec;           // x rows and every g allow 16-byte loads
+  const void* x;
+  void* t;            // T: fp32 with SPLIT, else bf16
+};
 
-// t[m, r]: one wave per latent row; grid.x = sum_b ceil(R_b / 4), grid.y = ceil(M / MT)
-template <typename XT, int MT>
-__global__ __launch_bounds__(kBlock) void latent_valu_kernel(ValuParams p) {
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int b = (p.nb > 1 && int(blockIdx.x) >= p.br[1].block0) ? 1 : 0;
-  const DevBranch B = pick(p, b);
-  const int r = (int(blockIdx.x) - B.block0) * kWavesPerBlock + wave;
-  if (r >= B.R) return;  // uniform per wave
-  const int m0 = int(blockIdx.y) * MT;
-  const XT* x = static_cast<const XT*>(p.x);
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
 
-  float acc[MT];
+// Rows [m0, m0 + 128) x k [k0, k0 + 32) of A (times g[k] when g is given):
+// thread tid holds 16-byte chunks tid and tid + 256 (row c / 4, k 8 * (c % 4)).
+// Rows past M repeat row M - 1; k past K reads as zero.
+template <typename AT, bool SPLIT>
+struct AStage {
+  float v[2][8];
+
+  __device__ __forceinline__ void load(const AT* __restrict__ A, int64_t lda, int M, int m0, int K, int k0,
+                                       const float* __restrict__ g, bool vec, int tid) {
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = 0.f;
-
-  const uint32_t* vrow = B.v + size_t(r) * p.KW;
-  for (int w = lane; w < p.KW; w += kWave) {
-    const uint32_t bits = vrow[w];
-    const int k0 = w * 32;
-    const int kn = min(32, p.K - k0);
-    for (int j = 0; j < kn; ++j) {
-      const float gk = B.g[k0 + j];
-      const bool neg = (bits >> j) & 1u;
+    for (int j = 0; j < 2; ++j) {
+      const int c = tid + kGThreads * j;
+      const int kk = k0 + 8 * (c & 3);
+      const int m = min(m0 + (c >> 2), M - 1);
+      const AT* __restrict__ src = A + int64_t(m) * lda + kk;
+      if (vec && kk + 8 <= K) {
+        load8(src, v[j]);
+        if (g) {
+          float gv[8];
+          load8(g + kk, gv);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int m = m0 + i;
-        if (m < p.M) {
-          const float a = gk * to_f32(x[size_t(m) * p.K + k0 + j]);
-          acc[i] += neg ? -a : a;
+          for (int i = 0; i < 8; ++i) v[j][i] *= gv[i];
         }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = (kk + i < K) ? to_f32(src[i]) * (g ? g[kk + i] : 1.f) : 0.f;
       }
     }
   }
+
+  __device__ __forceinline__ void store(unsigned short* hi, int tid) const {
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    float v = acc[i];
+    for (int j = 0; j < 2; ++j) {
+      const int c = tid + kGThreads * j;
+      const int off = (c >> 2) * kGRow + 8 * (c & 3);
+      if constexpr (SPLIT) {
+        u32x4 h, l;
+        split8(v[j], h, l);
+        *reinterpret_cast<u32x4*>(hi + off) = h;
+        *reinterpret_cast<u32x4*>(hi + kGTile + off) = l;
+      } else {
+        u32x4 h;
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    acc[i] = v;
-  }
-  if (lane == 0) {
-    const float lr = B.l[r];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int m = m0 + i;
-      if (m < p.M) B.t[size_t(m) * B.R + r] = lr * acc[i];
+        for (int d = 0; d < 4; ++d) h[d] = pack_bf16x2(v[j][2 * d], v[j][2 * d + 1]);
+        *reinterpret_cast<u32x4*>(hi + off) = h;
+      }
     }
+  }
+};
+
+// acc[i][j] += A[m0 + 64*wm + 32*i + .., :K] . S[:K, c0 + 64*wn + 32*j + ..]
+// over nks k-steps, S[k, c] = sign bit k of row c of W (ldw words per row).
+// lds: two buffers of (SPLIT ? 2 : 1) tiles.  Ends with a barrier.
+template <typename AT, bool SPLIT>
+__device__ __forceinline__ void gemm_mainloop(const AT* __restrict__ A, int64_t lda, int M, int m0, int K,
+                                              const float* __restrict__ g, bool vec, const uint32_t* __restrict__ W,
+                                              int ldw, int ncols, int c0, int nks, unsigned short* lds,
+                                              f32x16 (&acc)[2][2], int tid) {
+  constexpr int NT = SPLIT ? 2 : 1;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  const uint32_t* __restrict__ wrow[2];
+  bool cv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = c0 + 64 * wn + 32 * j + lr;
+    cv[j] = col < ncols;
+    wrow[j] = W + int64_t(cv[j] ? col : 0) * ldw;
+  }
+  AStage<AT, SPLIT> st;
+  st.load(A, lda, M, m0, K, 0, g, vec, tid);
+  uint32_t w[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) w[j] = cv[j] ? wrow[j][0] : 0u;
+  st.store(lds, tid);
+  __syncthreads();
+
+  uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
+  asm volatile("" : "+v"(kmask), "+v"(kone));
+  for (int ks = 0; ks < nks; ++ks) {
+    const bool more = ks + 1 < nks;
+    uint32_t wnext[2] = {0u, 0u};
+    if (more) {
+      st.load(A, lda, M, m0, K, (ks + 1) * kGK, g, vec, tid);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) wnext[j] = cv[j] ? wrow[j][ks + 1] : 0u;
+    }
+    const unsigned short* a = lds + (ks & 1) * NT * kGTile;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bf16x8 b[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = signs_to_bf16x8(w[j] >> (8 * lh), 2 * s, kmask, kone);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int off = (64 * wm + 32 * i + lr) * kGRow + 16 * s + 8 * lh;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(a + off);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b[j], acc[i][j], 0, 0, 0);
+        if constexpr (SPLIT) {
+          const bf16x8 al = *reinterpret_cast<const bf16x8*>(a + kGTile + off);
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      st.store(lds + ((ks + 1) & 1) * NT * kGTile, tid);
+      w[0] = wnext[0];
+      w[1] = wnext[1];
+    }
+    __syncthreads();
   }
 }
 
-// y[m, n]: LPR lanes per output row; grid.x = ceil(N / (256 / LPR)), grid.y = ceil(M / MT)
-template <typename YT, int MT, int LPR>
-__global__ __launch_bounds__(kBlock) void expand_valu_kernel(ValuParams p) {
-  extern __shared__ float lds_tv[];  // per branch [MT][R_b]
-  const int m0 = int(blockIdx.y) * MT;
+__device__ __forceinline__ void store_t(float* t, int64_t i, float v) { t[i] = v; }
+__device__ __forceinline__ void store_t(uint16_t* t, int64_t i, float v) { t[i] = f32_to_bf16(v); }
 
-  int off = 0;
-  for (int b = 0; b < p.nb; ++b) {
-    const DevBranch B = pick(p, b);
-    for (int i = threadIdx.x; i < MT * B.R; i += kBlock) {
-      const int mi = i / B.R;
-      const int r = i - mi * B.R;
-      const int m = m0 + mi;
-      lds_tv[off + i] = (m < p.M) ? B.t[size_t(m) * B.R + r] : 0.f;
-    }
-    off += MT * B.R;
-  }
-  __syncthreads();
+// Stage 1.  grid = (m-tiles, column tiles of all segments), 256 threads.
+template <typename XT, bool SPLIT>
+__global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
+  using TT = typename std::conditional<SPLIT, float, uint16_t>::type;
+  extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
+  const int tid = int(threadIdx.x);
+  const int nt = int(blockIdx.y);
+  int si = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSeg; ++i) si += (i < p.nseg && nt >= p.seg[i].nt0) ? 1 : 0;
+  si = __builtin_amdgcn_readfirstlane(si);
+  const GemmSeg& S = p.seg[si];
+  const int m0 = int(blockIdx.x) * kGB;
+  const int c0 = (nt - S.nt0) * kGB;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  gemm_mainloop<XT, SPLIT>(static_cast<const XT*>(p.x), p.K, p.M, m0, p.K, S.g, p.xvec != 0, S.V, p.KW, S.R, c0,
+                           p.KW, glds, acc, tid);
 
-  const int n = int(blockIdx.x) * (kBlock / LPR) + int(threadIdx.x) / LPR;
-  const int q = int(threadIdx.x) % LPR;
-  float out[MT];
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  TT* __restrict__ T = static_cast<TT*>(p.t) + S.tbase;
 #pragma unroll
-  for (int i = 0; i < MT; ++i) out[i] = 0.f;
-
-  off = 0;
-  for (int b = 0; b < p.nb; ++b) {
-    const DevBranch B = pick(p, b);
-    float acc[MT];
+  for (int j = 0; j < 2; ++j) {
+    const int r = c0 + 64 * wn + 32 * j + lr;  // < RP; rows R <= r < RP are written as zeros
+    const float lv = r < S.R ? S.l[r] : 0.f;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = 0.f;
-    if (n < p.N) {
-      const uint32_t* urow = B.u + size_t(n) * B.RW;
-      for (int w = q; w < B.RW; w += LPR) {
-        const uint32_t bits = urow[w];
-        const int r0 = w * 32;
-        const int rn = min(32, B.R - r0);
-        for (int j = 0; j < rn; ++j) {
-          const bool neg = (bits >> j) & 1u;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            const float tv = lds_tv[off + i * B.R + r0 + j];
-            acc[i] += neg ? -tv : tv;
-          }
-        }
+      for (int q = 0; q < 16; ++q) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+        if (m < p.M) store_t(T, int64_t(m) * S.RP + r, lv * acc[i][j][q]);
       }
-    }
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      float v = acc[i];
-#pragma unroll
-      for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
-      acc[i] = v;
-    }
-    const float hn = (n < p.N) ? B.h[n] : 0.f;
-#pragma unroll
-    for (int i = 0; i < MT; ++i) out[i] += hn * acc[i];
-    off += MT * B.R;
   }
+}
 
-  if (n < p.N && q == 0) {
-    const float bn = p.bias ? p.bias[n] : 0.f;
-    YT* y = static_cast<YT*>(p.y);
+// Stage 2.  grid = (m-tiles, column tiles of all projections), 256 threads.
+template <typename YT, bool SPLIT>
+__global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
+  using TT = typename std::conditional<SPLIT, float, uint16_t>::type;
+  extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
+  const int tid = int(threadIdx.x);
+  const int nt = int(blockIdx.y);
+  int pi = 0;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int m = m0 + i;
-      if (m < p.M) store_out(y, size_t(m) * p.N + n, out[i] + bn);
-    }
+  for (int i = 1; i < kMaxProj; ++i) pi += (i < p.nproj && nt >= p.proj[i].nt0) ? 1 : 0;
+  pi = __builtin_amdgcn_readfirstlane(pi);
+  const GemmProj& P = p.proj[pi];
+  const int m0 = int(blockIdx.x) * kGB;
+  const int c0 = (nt - P.nt0) * kGB;
+  const TT* __restrict__ T = static_cast<const TT*>(p.t);
+  f32x16 acc0[2][2], acc1[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc0[i][j] = acc1[i][j] = f32x16{};
+  gemm_mainloop<TT, SPLIT>(T + P.tbase[0], P.RP[0], p.M, m0, kGK * P.RW[0], nullptr, true, P.U[0], P.RW[0], P.N, c0,
+                           P.RW[0], glds, acc0, tid);
+  if (P.nb > 1)
+    gemm_mainloop<TT, SPLIT>(T + P.tbase[1], P.RP[1], p.M, m0, kGK * P.RW[1], nullptr, true, P.U[1], P.RW[1], P.N,
+                             c0, P.RW[1], glds, acc1, tid);
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  YT* __restrict__ y = static_cast<YT*>(P.y);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = c0 + 64 * wn + 32 * j + lr;
+    if (n >= P.N) continue;
+    const float h0 = P.h[0][n];
+    const float h1 = P.nb > 1 ? P.h[1][n] : 0.f;
+    const float bn = P.bias ? P.bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+        if (m < p.M) store_out(y, size_t(m) * P.N + n, h0 * acc0[i][j][q] + h1 * acc1[i][j][q] + bn);
+      }
   }
 }
 
@@ -786,10 +909,10 @@ int validate_group(const ProjDesc* pd, int np, int64_t M, int64_t K) {
 // workspace keep its invariants:
 //   [0, kCounterBytes)                 latent-buffer state (see MfmaParams)
 //   [kTOffset, kTOffset + kTBytes)     MFMA-path latent halves
-//   [kValuOffset, ...)                 general-path latent buffers
+//   [kGemmOffset, ...)                 GEMM-path T
 constexpr size_t kTOffset = 4096;
 constexpr size_t kTBytes = 2 * size_t(kTHalf) * sizeof(float);
-constexpr size_t kValuOffset = kTOffset + kTBytes;
+constexpr size_t kGemmOffset = kTOffset + kTBytes;
 static_assert(kCounterBytes <= kTOffset, "counter region overlaps t");
 
 // Launch plan shared by the workspace query and the forward.
@@ -812,25 +935,32 @@ size_t compact_rows(int mt, int64_t nch) {
   return size_t(mb) * size_t(nch) * size_t(2 * mr + 1);
 }
 
+size_t gemm_lds_bytes(bool split) { return size_t(2) * (split ? 2 : 1) * kGTile * sizeof(uint16_t); }
+
+// T of the GEMM path: per segment [M][RP] (fp32 with SPLIT, else bf16).
+size_t gemm_t_bytes(const ProjDesc* pd, int np, int64_t M, bool split) {
+  size_t n = 0;
+  for (int q = 0; q < np; ++q)
+    for (int b = 0; b < pd[q].nb; ++b) n += size_t(M) * size_t(ceil_div(pd[q].br[b].rank, kGB) * kGB);
+  return align256(n * (split ? sizeof(float) : sizeof(uint16_t)));
+}
+
 Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   Plan pl{};
   int64_t nrb = 0, steps_max = 0;
-  size_t lds2 = 0, valu_bytes = 0;
+  size_t lds2 = 0;
   pl.mt = mtile(M);
   for (int q = 0; q < np; ++q) {
     int64_t rwp_sum = 0;
-    size_t vb = 0;
     for (int b = 0; b < pd[q].nb; ++b) {
       const int64_t R = pd[q].br[b].rank;
       rwp_sum += ceil_div(ceil_div(R, 32), 4) * 4;
       nrb += ceil_div(R, kRowBlock);
-      vb += align256(size_t(M) * size_t(R) * sizeof(float));
     }
     const size_t l2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
     if (l2 > lds2) lds2 = l2;
     const int64_t ws = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
     if (ws > steps_max) steps_max = ws;
-    if (vb > valu_bytes) valu_bytes = vb;
   }
   pl.nrb = int(nrb);
   pl.mfma = (M >= 1 && M <= kMaxMfmaM && lds2 <= size_t(kMaxLds) && steps_max <= kMaxWaveSteps);
@@ -846,7 +976,7 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     pl.lds2 = lds2;
     pl.ws_total = kTOffset + kTBytes;
   } else {
-    pl.ws_total = kValuOffset + valu_bytes;
+    pl.ws_total = kGemmOffset + gemm_t_bytes(pd, np, M, true);
   }
   return pl;
 }
@@ -967,93 +1097,66 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   return check_launch("expand_mfma_kernel");
 }
 
-template <typename XT>
-void launch_latent_valu(const ValuParams& p, int mt, dim3 grid, hipStream_t s) {
-  switch (mt) {
-    case 1: hipLaunchKernelGGL((latent_valu_kernel<XT, 1>), grid, dim3(kBlock), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((latent_valu_kernel<XT, 2>), grid, dim3(kBlock), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((latent_valu_kernel<XT, 4>), grid, dim3(kBlock), 0, s, p); break;
-    default: hipLaunchKernelGGL((latent_valu_kernel<XT, 8>), grid, dim3(kBlock), 0, s, p); break;
-  }
-}
-
-template <typename YT, int MT>
-void launch_expand_valu_lpr(const ValuParams& p, int lpr, size_t lds, hipStream_t s) {
-  const int rows = kBlock / lpr;
-  const dim3 grid{unsigned(ceil_div(p.N, rows)), unsigned(ceil_div(p.M, MT)), 1u};
-  switch (lpr) {
-    case 4: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 4>), grid, dim3(kBlock), lds, s, p); break;
-    case 16: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 16>), grid, dim3(kBlock), lds, s, p); break;
-    default: hipLaunchKernelGGL((expand_valu_kernel<YT, MT, 64>), grid, dim3(kBlock), lds, s, p); break;
-  }
-}
-
-template <typename YT>
-void launch_expand_valu(const ValuParams& p, int mt, int lpr, size_t lds, hipStream_t s) {
-  switch (mt) {
-    case 1: launch_expand_valu_lpr<YT, 1>(p, lpr, lds, s); break;
-    case 2: launch_expand_valu_lpr<YT, 2>(p, lpr, lds, s); break;
-    case 4: launch_expand_valu_lpr<YT, 4>(p, lpr, lds, s); break;
-    default: launch_expand_valu_lpr<YT, 8>(p, lpr, lds, s); break;
-  }
-}
-
-int mtile_for(int64_t M, int64_t cap) {
-  int mt = 8;
-  while (mt > 1 && (mt > cap || (mt / 2) >= M)) mt /= 2;
-  return mt;
-}
-
-int forward_valu(const lbk_branch* branches, int nb, int64_t M, int64_t K, int64_t N, const void* x,
-                 int x_dtype, const float* bias, void* y, int y_dtype, void* workspace, hipStream_t s) {
-  ValuParams p;
+int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, int y_dtype,
+                 void* workspace, hipStream_t s) {
+  const bool split = x_dtype == LBK_F32;
+  GemmParams p;
   memset(&p, 0, sizeof(p));
-  p.nb = nb;
+  p.nproj = np;
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
-  p.N = int(N);
   p.x = x;
-  p.bias = bias;
-  p.y = y;
-  char* ws = static_cast<char*>(workspace) + kValuOffset;  // counters and t stay untouched
-  int blocks = 0;
-  int64_t rsum = 0;
-  int rw_max = 0;
-  for (int b = 0; b < nb; ++b) {
-    const lbk_branch& S = branches[b];
-    DevBranch& D = p.br[b];
-    D.v = reinterpret_cast<const uint32_t*>(S.v_sign);
-    D.u = reinterpret_cast<const uint32_t*>(S.u_sign);
-    D.g = S.v2;
-    D.l = S.mid;
-    D.h = S.u1;
-    D.R = int(S.rank);
-    D.RW = int(ceil_div(S.rank, 32));
-    D.t = reinterpret_cast<float*>(ws);
-    ws += align256(size_t(M) * size_t(S.rank) * sizeof(float));
-    D.block0 = blocks;
-    blocks += int(ceil_div(S.rank, kWavesPerBlock));
-    rsum += S.rank;
-    if (D.RW > rw_max) rw_max = D.RW;
+  p.t = static_cast<char*>(workspace) + kGemmOffset;
+  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  int si = 0, nt1 = 0, nt2 = 0;
+  int64_t tbase = 0;
+  for (int q = 0; q < np; ++q) {
+    GemmProj& P = p.proj[q];
+    P.nb = pd[q].nb;
+    P.N = int(pd[q].N);
+    P.bias = pd[q].bias;
+    P.y = pd[q].y;
+    P.nt0 = nt2;
+    nt2 += int(ceil_div(pd[q].N, kGB));
+    for (int b = 0; b < pd[q].nb; ++b, ++si) {
+      const lbk_branch& B = pd[q].br[b];
+      GemmSeg& S = p.seg[si];
+      S.V = reinterpret_cast<const uint32_t*>(B.v_sign);
+      S.g = B.v2;
+      S.l = B.mid;
+      S.R = int(B.rank);
+      S.RP = int(ceil_div(B.rank, kGB) * kGB);
+      S.nt0 = nt1;
+      S.tbase = tbase;
+      nt1 += S.RP / kGB;
+      P.U[b] = reinterpret_cast<const uint32_t*>(B.u_sign);
+      P.h[b] = B.u1;
+      P.RW[b] = int(ceil_div(B.rank, 32));
+      P.RP[b] = S.RP;
+      P.tbase[b] = tbase;
+      tbase += M * S.RP;
+      xvec = xvec && (reinterpret_cast<uintptr_t>(B.v2) % 16) == 0;
+    }
   }
-  const int mt1 = mtile_for(M, 8);
-  const int64_t mchunks1 = ceil_div(M, mt1);
-  if (mchunks1 > 65535) return set_error(LBK_ERR_ARG, "M=%lld too large for this path", (long long)M);
-  const dim3 g1{unsigned(blocks), unsigned(mchunks1), 1u};
-  if (x_dtype == LBK_F32) launch_latent_valu<float>(p, mt1, g1, s);
-  else launch_latent_valu<uint16_t>(p, mt1, g1, s);
-  int rc = check_launch("latent_valu_kernel");
+  p.nseg = si;
+  p.xvec = xvec ? 1 : 0;
+  const int64_t mtiles = ceil_div(M, kGB);
+  if (nt1 > 65535 || nt2 > 65535) return set_error(LBK_ERR_ARG, "too many column tiles for the GEMM path");
+  const size_t lds = gemm_lds_bytes(split);
+  const dim3 g1{unsigned(mtiles), unsigned(nt1), 1u}, g2{unsigned(mtiles), unsigned(nt2), 1u};
+  if (split) hipLaunchKernelGGL((gemm_latent_kernel<float, true>), g1, dim3(kGThreads), lds, s, p);
+  else hipLaunchKernelGGL((gemm_latent_kernel<uint16_t, false>), g1, dim3(kGThreads), lds, s, p);
+  int rc = check_launch("gemm_latent_kernel");
   if (rc != LBK_OK) return rc;
-
-  const int64_t cap = kValuLdsBudget / (rsum * int64_t(sizeof(float)));
-  const int mt2 = mtile_for(M, cap < 1 ? 1 : cap);
-  if (ceil_div(M, mt2) > 65535) return set_error(LBK_ERR_ARG, "M=%lld too large for this path", (long long)M);
-  const size_t lds = size_t(rsum) * mt2 * sizeof(float);
-  const int lpr = rw_max <= 8 ? 4 : (rw_max <= 32 ? 16 : 64);
-  if (y_dtype == LBK_F32) launch_expand_valu<float>(p, mt2, lpr, lds, s);
-  else launch_expand_valu<uint16_t>(p, mt2, lpr, lds, s);
-  return check_launch("expand_valu_kernel");
+  if (split) {
+    if (y_dtype == LBK_F32) hipLaunchKernelGGL((gemm_expand_kernel<float, true>), g2, dim3(kGThreads), lds, s, p);
+    else hipLaunchKernelGGL((gemm_expand_kernel<uint16_t, true>), g2, dim3(kGThreads), lds, s, p);
+  } else {
+    if (y_dtype == LBK_F32) hipLaunchKernelGGL((gemm_expand_kernel<float, false>), g2, dim3(kGThreads), lds, s, p);
+    else hipLaunchKernelGGL((gemm_expand_kernel<uint16_t, false>), g2, dim3(kGThreads), lds, s, p);
+  }
+  return check_launch("gemm_expand_kernel");
 }
 
 int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, int y_dtype,
@@ -1071,11 +1174,7 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
     return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.mfma) return forward_mfma(pd, np, pl, M, K, x, x_dtype, y_dtype, workspace, s);
-  for (int q = 0; q < np; ++q) {
-    rc = forward_valu(pd[q].br, pd[q].nb, M, K, pd[q].N, x, x_dtype, pd[q].bias, pd[q].y, y_dtype, workspace, s);
-    if (rc != LBK_OK) return rc;
-  }
-  return LBK_OK;
+  return forward_gemm(pd, np, M, K, x, x_dtype, y_dtype, workspace, s);
 }
 
 }  // namespace

@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 TOL_F32 = 1e-3
 TOL_BF16_OUT = 4e-3
+TOL_BF16_PREFILL = 5e-3  # bf16 activations at M > 16: bf16 MFMA operands
 
 
 def _dev_branch(b, dev):
@@ -143,10 +144,30 @@ def test_bf16_in_bf16_out(gpu):
 
 
 def test_prefill_shape_small(gpu):
+    """bf16 activations at M > 16 take the bf16 GEMM path (config 4 shape, fewer tokens)."""
     K, N = 4096, 4096
     x, brs = _synthetic(1006, 256, K, N, [204, 1843])
     y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.float32)
-    _check(y, xu, brs, K, N, TOL_F32, what="M=256")
+    _check(y, xu, brs, K, N, TOL_BF16_PREFILL, what="bf16 M=256")
+
+
+@pytest.mark.parametrize("M,K,N,ranks", [(512, 4096, 1024, [81, 737]), (130, 14336, 4096, [318]),
+                                         (200, 4096, 14336, [318, 2867])])
+def test_prefill_bf16_llama3_shapes(gpu, M, K, N, ranks):
+    x, brs = _synthetic(1010 + M, M, K, N, ranks)
+    y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.bfloat16)
+    _check(y, xu, brs, K, N, TOL_BF16_PREFILL, what=f"bf16 M={M} K={K} N={N} R={ranks}")
+
+
+@pytest.mark.parametrize("M,K,N,ranks", [(32, 4096, 4096, [205, 1843]), (17, 4096, 11008, [298, 2686]),
+                                         (64, 11008, 4096, [298, 2686]), (33, 70, 45, [37, 5]),
+                                         (129, 1000, 300, [130]), (8, 4096, 4096, [4000, 4000])])
+def test_gemm_path_fp32(gpu, M, K, N, ranks):
+    """fp32 activations at M > 16 (tree verify) or with operands too large for
+    the decode kernels' LDS: hi/lo-split GEMM path, fp32 tolerance."""
+    x, brs = _synthetic(1020 + M, M, K, N, ranks)
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=f"fp32 gemm M={M} K={K} N={N} R={ranks}")
 
 
 def test_empty_batch(gpu):
