@@ -162,6 +162,60 @@ def call_duration_us(gen, dev, names, stream, count=32, steps=100, warmup=10):
     return calls[0], ms * 1000.0 / count
 
 
+# Llama-3-8B-shaped prefill, draft 0.1 BPW + residual 0.9 BPW
+# per projection (ranks floor(bpw*K*N/(K+N))), M = 2048 bf16 tokens.
+PREFILL_M = 2048
+PREFILL_LAYER = [("qkv", [(4096, 4096, [204, 1843]), (4096, 1024, [81, 737]), (4096, 1024, [81, 737])]),
+                 ("o", [(4096, 4096, [204, 1843])]),
+                 ("gate/up", [(4096, 14336, [318, 2867]), (4096, 14336, [318, 2867])]),
+                 ("down", [(14336, 4096, [318, 2867])])]
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def proj_flops(M, K, N, ranks):
+    return sum(2 * M * (R * K + N * R) for R in ranks)
+
+
+class PrefillLayer:
+    """One decoder layer's linears at M tokens (bf16 in, bf16 out), as calls."""
+
+    def __init__(self, gen, dev, M):
+        import torch
+        from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+        self.calls = []
+        self.flops = 0
+        for kind, shapes in PREFILL_LAYER:
+            projs = [LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
+                     for K, N, ranks in shapes]
+            K = shapes[0][0]
+            x = torch.randn((M, K), generator=gen).to(torch.bfloat16).to(dev)
+            outs = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _, N, _ in shapes]
+            self.calls.append((kind, LittleBitProjectionGroup(projs), x, outs))
+            self.flops += sum(proj_flops(M, K, N, ranks) for K, N, ranks in shapes)
+
+    def run(self, only=None):
+        for kind, grp, x, outs in self.calls:
+            if only is None or kind == only:
+                grp.forward(x, outs=outs)
+
+
+def prefill_bench(gen, dev, stream, steps=20, warmup=3):
+    """ms per layer and TFLOP/s of the config-4 linears (2 layers' weights rotated)."""
+    layers = [PrefillLayer(gen, dev, PREFILL_M) for _ in range(2)]
+    graphs = [capture(l.run, stream) for l in layers]
+    ms = time_graphs(graphs, steps, warmup, stream)
+    per_call = {}
+    for kind, _ in PREFILL_LAYER:
+        g = [capture(lambda l=l: l.run(kind), stream) for l in layers]
+        per_call[kind] = round(time_graphs(g, steps, warmup, stream) * 1000.0, 2)
+    tflops = layers[0].flops / (ms * 1e-3) / 1e12
+    return {"workload": "llama3-8b prefill linears, 1 layer (q/k/v, o, gate/up, down; draft + residual branches)",
+            "M": PREFILL_M, "dtype": "bf16", "ms_per_layer": round(ms, 4),
+            "ms_per_forward_32_layers": round(32 * ms, 3), "flops_per_layer": layers[0].flops,
+            "tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "us_per_call": per_call}
+
+
 def cpu_baseline(layers, budget_s=12.0):
     """The reference littlebit_linear (int8-quantised AVX2) over whole draft
     steps on the host cores, within a time budget."""
@@ -214,7 +268,8 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down"], default=None,
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
+    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -231,6 +286,9 @@ def main():
 
     gen = torch.Generator().manual_seed(1002)
     kinds = dict(LAYER_CALLS)
+    if args.only == "prefill":
+        print(json.dumps(prefill_bench(gen, dev, stream, args.steps, args.warmup)))
+        return
     if args.only:
         names = kinds[args.only.replace("gate_up", "gate/up")]
         call, us = call_duration_us(gen, dev, names, stream, args.layers, args.steps, args.warmup)
@@ -264,6 +322,7 @@ def main():
                 "kernel": f"LittleBitLinear {dom} call ({d['projections']}): latent_mfma_kernel + expand_mfma_kernel",
                 "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_call"]}
 
+    prefill = None if args.no_prefill else prefill_bench(gen, dev, stream)
     cpu = None if args.no_cpu else cpu_baseline(args.layers, args.cpu_budget)
     value = step_bytes / (ms_cold * 1e-3) / 1e9
     out = {
@@ -295,6 +354,7 @@ def main():
         "per_class": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in cls_stats.items()},
         "roofline": roofline,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

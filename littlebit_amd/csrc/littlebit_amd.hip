@@ -26,7 +26,8 @@
 //                       of its 16 rows and accumulates both branches, then
 //                       writes h0*y0 + h1*y1 + bias.
 // GEMM path (M > 16, or operands too large for the decode path's LDS):
-//   gemm_latent_kernel / gemm_expand_kernel, tiled on v_mfma_f32_32x32x16_bf16.
+//   gemm_scale_kernel (bf16 g*x) / gemm_latent_kernel / gemm_expand_kernel,
+//   tiled on v_mfma_f32_32x32x16_bf16.
 //
 // Splitting fp32 activations into bf16 hi + lo keeps the product error near
 // 2^-17 relative: +-1 is exact in bf16 and the MFMA accumulates in fp32.
@@ -557,24 +558,27 @@ __global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(M
 
 // ---------------------------------------------------------------------------
 // GEMM path (M > 16, and shapes the decode path cannot stage in LDS): a
-// tiled sign-GEMM on v_mfma_f32_32x32x16_bf16.
-//   stage 1  T[m, r] = l[r] * sum_k sV[r, k] * g[k] * x[m, k]
-//   stage 2  y[m, n] = bias[n] + sum_b h_b[n] * sum_r sU_b[n, r] * T_b[m, r]
-// Block tile 128 (m) x 128 (columns: latent rows in stage 1, outputs in
-// stage 2), 4 waves of 64 x 64 (2 x 2 MFMA tiles), k-steps of 32.  The A
-// tile (activations) is staged in LDS as bf16, double-buffered; the +-1 B
-// operand is expanded in registers from the sign word of the lane's column:
-// for sub-step s of a k-step, lane l (column l % 32, k 8*(l/32) .. +8 of
-// the 32x32x16 operand) takes byte 2*s + l/32 of that word.
-// SPLIT (fp32 activations): A is staged as bf16 hi and lo tiles, both go
-// through the MFMA, so products keep ~2^-17 relative error; T is fp32.
-// Without SPLIT (bf16 activations): A = bf16(g*x) and T is bf16, the
-// precision of the reference's bf16 forward (littlebit.py:116-121).
+// tiled sign-GEMM on v_mfma_f32_32x32x16_bf16, three launches per call.
+//   prologue  A_s[m, k] = g_s[k] * x[m, k] per branch s, as bf16, k padded
+//             with zeros to a multiple of 64
+//   stage 1   T_s[m, r] = l_s[r] * sum_k sV_s[r, k] * A_s[m, k], as bf16
+//   stage 2   y[m, n] = bias[n] + sum_b h_b[n] * sum_r sU_b[n, r] * T_b[m, r]
+// With SPLIT (fp32 activations) A and T are stored as two bf16 planes, hi
+// and lo = bf16(v - hi), and both planes go through the MFMA, so products
+// keep ~2^-17 relative error.  Without SPLIT (bf16 activations) one plane:
+// the precision of the reference's bf16 forward (littlebit.py:116-121).
+// Stages 1 and 2: block tile 128 (m) x 128 (columns: latent rows in stage
+// 1, outputs in stage 2), 4 waves of 64 x 64 (2 x 2 MFMA tiles), k-steps of
+// 64.  A tiles go to LDS by plain 16-byte copies, double-buffered; the +-1 B
+// operand is expanded in registers from the sign words of the lane's
+// column: for 16-k sub-step s, lane l (column l % 32, k 8*(l/32) .. +8 of
+// the 32x32x16 operand) takes byte 2*(s%2) + l/32 of word s/2 of the step.
 // ---------------------------------------------------------------------------
 constexpr int kGB = 128;             // block tile (m and columns)
-constexpr int kGK = 32;              // k per step
+constexpr int kGK = 64;              // k per step (two sign words per column)
 constexpr int kGThreads = 256;
-constexpr int kGRow = 40;            // bf16 per LDS row: 32 + 8 pad (80 B rows, 16-byte aligned)
+constexpr int kGChunks = kGB * kGK / 8 / kGThreads;  // 16-byte A chunks per thread per step
+constexpr int kGRow = kGK + 8;       // bf16 per LDS row: 144 B, 16-byte aligned, rows 36 banks apart
 constexpr int kGTile = kGB * kGRow;  // bf16 per LDS tile
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -586,7 +590,8 @@ struct GemmSeg {      // stage-1 operands of one branch
   int R;
   int RP;             // T row length: R rounded up to kGB
   int nt0;            // first column tile of the segment
-  int64_t tbase;      // element offset of the segment's [M][RP] block of T
+  int64_t abase;      // offset of the segment's [M][Kp] block in an A plane
+  int64_t tbase;      // offset of the segment's [M][RP] block in a T plane
 };
 
 struct GemmProj {     // stage-2 operands of one projection
@@ -594,7 +599,7 @@ struct GemmProj {     // stage-2 operands of one projection
   const float* h[2];
   const float* bias;
   void* y;
-  int RW[2];          // words per U row = k-steps of stage 2
+  int RW[2];          // words per U row
   int RP[2];
   int64_t tbase[2];
   int nb;
@@ -607,74 +612,96 @@ struct GemmParams {
   GemmProj proj[kMaxProj];
   int nseg, nproj;
   int M, K, KW;
+  int Kp;             // K rounded up to kGK
   int xvec;           // x rows and every g allow 16-byte loads
   const void* x;
-  void* t;            // T: fp32 with SPLIT, else bf16
+  uint16_t* a;        // A planes (hi, then lo with SPLIT)
+  uint16_t* t;        // T planes
+  int64_t a_plane;    // elements per A plane
+  int64_t t_plane;    // elements per T plane
 };
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const f32x2 v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+// hi = bf16(v), lo = bf16(v - hi), round to nearest even
+__device__ __forceinline__ void split1(float v, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16(v);
+  lo = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
-// Rows [m0, m0 + 128) x k [k0, k0 + 32) of A (times g[k] when g is given):
-// thread tid holds 16-byte chunks tid and tid + 256 (row c / 4, k 8 * (c % 4)).
-// Rows past M repeat row M - 1; k past K reads as zero.
-template <typename AT, bool SPLIT>
-struct AStage {
-  float v[2][8];
+// Prologue.  grid = (M, segments), 256 threads; thread handles 8-k chunks.
+template <typename XT, bool SPLIT>
+__global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
+  const int m = int(blockIdx.x);
+  const GemmSeg& S = p.seg[__builtin_amdgcn_readfirstlane(int(blockIdx.y))];
+  const XT* __restrict__ xr = static_cast<const XT*>(p.x) + int64_t(m) * p.K;
+  const float* __restrict__ g = S.g;
+  uint16_t* __restrict__ hi = p.a + S.abase + int64_t(m) * p.Kp;
+  for (int k = 8 * int(threadIdx.x); k < p.Kp; k += 8 * kGThreads) {
+    float v[8];
+    if (p.xvec && k + 8 <= p.K) {
+      float gv[8];
+      load8(xr + k, v);
+      load8(g + k, gv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] *= gv[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (k + i < p.K) ? g[k + i] * to_f32(xr[k + i]) : 0.f;
+    }
+    if constexpr (SPLIT) {
+      u32x4 h, l;
+      split8(v, h, l);
+      *reinterpret_cast<u32x4*>(hi + k) = h;
+      *reinterpret_cast<u32x4*>(hi + p.a_plane + k) = l;
+    } else {
+      u32x4 h;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) h[d] = uint32_t(f32_to_bf16(v[2 * d])) | (uint32_t(f32_to_bf16(v[2 * d + 1])) << 16);
+      *reinterpret_cast<u32x4*>(hi + k) = h;
+    }
+  }
+}
 
-  __device__ __forceinline__ void load(const AT* __restrict__ A, int64_t lda, int M, int m0, int K, int k0,
-                                       const float* __restrict__ g, bool vec, int tid) {
+// Rows [m0, m0 + 128) x k [k0, k0 + 64) of the bf16 planes of A (lda >= k0 +
+// 64): thread tid copies 16-byte chunks c = tid + 256 * j (row c / 8, k
+// 8 * (c % 8)).  load() issues the loads, store() writes LDS, so the loads
+// of the next step stay in flight across this step's MFMAs.  Rows past M
+// repeat row M - 1.
+template <bool SPLIT>
+struct AStage {
+  u32x4 raw[kGChunks][SPLIT ? 2 : 1];
+
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ A, int64_t plane, int64_t lda, int M, int m0,
+                                       int k0, int tid) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kGChunks; ++j) {
       const int c = tid + kGThreads * j;
-      const int kk = k0 + 8 * (c & 3);
-      const int m = min(m0 + (c >> 2), M - 1);
-      const AT* __restrict__ src = A + int64_t(m) * lda + kk;
-      if (vec && kk + 8 <= K) {
-        load8(src, v[j]);
-        if (g) {
-          float gv[8];
-          load8(g + kk, gv);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) v[j][i] *= gv[i];
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[j][i] = (kk + i < K) ? to_f32(src[i]) * (g ? g[kk + i] : 1.f) : 0.f;
-      }
+      const int m = min(m0 + (c >> 3), M - 1);
+      const uint16_t* __restrict__ src = A + int64_t(m) * lda + k0 + 8 * (c & 7);
+      raw[j][0] = *reinterpret_cast<const u32x4*>(src);
+      if constexpr (SPLIT) raw[j][1] = *reinterpret_cast<const u32x4*>(src + plane);
     }
   }
 
-  __device__ __forceinline__ void store(unsigned short* hi, int tid) const {
+  __device__ __forceinline__ void store(unsigned short* lds, int tid) const {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kGChunks; ++j) {
       const int c = tid + kGThreads * j;
-      const int off = (c >> 2) * kGRow + 8 * (c & 3);
-      if constexpr (SPLIT) {
-        u32x4 h, l;
-        split8(v[j], h, l);
-        *reinterpret_cast<u32x4*>(hi + off) = h;
-        *reinterpret_cast<u32x4*>(hi + kGTile + off) = l;
-      } else {
-        u32x4 h;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) h[d] = pack_bf16x2(v[j][2 * d], v[j][2 * d + 1]);
-        *reinterpret_cast<u32x4*>(hi + off) = h;
-      }
+      const int off = (c >> 3) * kGRow + 8 * (c & 7);
+      *reinterpret_cast<u32x4*>(lds + off) = raw[j][0];
+      if constexpr (SPLIT) *reinterpret_cast<u32x4*>(lds + kGTile + off) = raw[j][1];
     }
   }
 };
 
-// acc[i][j] += A[m0 + 64*wm + 32*i + .., :K] . S[:K, c0 + 64*wn + 32*j + ..]
-// over nks k-steps, S[k, c] = sign bit k of row c of W (ldw words per row).
-// lds: two buffers of (SPLIT ? 2 : 1) tiles.  Ends with a barrier.
-template <typename AT, bool SPLIT>
-__device__ __forceinline__ void gemm_mainloop(const AT* __restrict__ A, int64_t lda, int M, int m0, int K,
-                                              const float* __restrict__ g, bool vec, const uint32_t* __restrict__ W,
-                                              int ldw, int ncols, int c0, int nks, unsigned short* lds,
-                                              f32x16 (&acc)[2][2], int tid) {
+// acc[i][j] += A[m0 + 64*wm + 32*i + .., :64*nks] . S[:64*nks, c0 + 64*wn + 32*j + ..]
+// S[k, c] = sign bit k of row c of W (ldw words per row, zero past it);
+// step ks reads words 2*ks and 2*ks + 1.  lds: two buffers of (SPLIT ? 2 : 1)
+// tiles.  Ends with a barrier.  (Loading two steps ahead instead of one
+// costs registers enough to halve the occupancy, which measured slower.)
+template <bool SPLIT>
+__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t plane, int64_t lda, int M,
+                                              int m0, const uint32_t* __restrict__ W, int ldw, int ncols, int c0,
+                                              int nks, unsigned short* lds, f32x16 (&acc)[2][2], int tid) {
   constexpr int NT = SPLIT ? 2 : 1;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -688,11 +715,19 @@ __device__ __forceinline__ void gemm_mainloop(const AT* __restrict__ A, int64_t 
     cv[j] = col < ncols;
     wrow[j] = W + int64_t(cv[j] ? col : 0) * ldw;
   }
-  AStage<AT, SPLIT> st;
-  st.load(A, lda, M, m0, K, 0, g, vec, tid);
-  uint32_t w[2];
+  auto load_words = [&](int ks, uint32_t (&w)[2][2]) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) w[j] = cv[j] ? wrow[j][0] : 0u;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int wi = 2 * ks + h;
+        w[j][h] = (cv[j] && wi < ldw) ? wrow[j][wi] : 0u;
+      }
+  };
+  AStage<SPLIT> st;
+  st.load(A, plane, lda, M, m0, 0, tid);
+  uint32_t w[2][2];
+  load_words(0, w);
   st.store(lds, tid);
   __syncthreads();
 
@@ -700,18 +735,17 @@ __device__ __forceinline__ void gemm_mainloop(const AT* __restrict__ A, int64_t 
   asm volatile("" : "+v"(kmask), "+v"(kone));
   for (int ks = 0; ks < nks; ++ks) {
     const bool more = ks + 1 < nks;
-    uint32_t wnext[2] = {0u, 0u};
+    uint32_t wnext[2][2] = {{0u, 0u}, {0u, 0u}};
     if (more) {
-      st.load(A, lda, M, m0, K, (ks + 1) * kGK, g, vec, tid);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) wnext[j] = cv[j] ? wrow[j][ks + 1] : 0u;
+      st.load(A, plane, lda, M, m0, (ks + 1) * kGK, tid);
+      load_words(ks + 1, wnext);
     }
     const unsigned short* a = lds + (ks & 1) * NT * kGTile;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < 4; ++s) {
       bf16x8 b[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) b[j] = signs_to_bf16x8(w[j] >> (8 * lh), 2 * s, kmask, kone);
+      for (int j = 0; j < 2; ++j) b[j] = signs_to_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask, kone);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int off = (64 * wm + 32 * i + lr) * kGRow + 16 * s + 8 * lh;
@@ -728,20 +762,19 @@ __device__ __forceinline__ void gemm_mainloop(const AT* __restrict__ A, int64_t 
     }
     if (more) {
       st.store(lds + ((ks + 1) & 1) * NT * kGTile, tid);
-      w[0] = wnext[0];
-      w[1] = wnext[1];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        w[j][0] = wnext[j][0];
+        w[j][1] = wnext[j][1];
+      }
     }
     __syncthreads();
   }
 }
 
-__device__ __forceinline__ void store_t(float* t, int64_t i, float v) { t[i] = v; }
-__device__ __forceinline__ void store_t(uint16_t* t, int64_t i, float v) { t[i] = f32_to_bf16(v); }
-
 // Stage 1.  grid = (m-tiles, column tiles of all segments), 256 threads.
-template <typename XT, bool SPLIT>
+template <bool SPLIT>
 __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
-  using TT = typename std::conditional<SPLIT, float, uint16_t>::type;
   extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
@@ -757,13 +790,12 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-  gemm_mainloop<XT, SPLIT>(static_cast<const XT*>(p.x), p.K, p.M, m0, p.K, S.g, p.xvec != 0, S.V, p.KW, S.R, c0,
-                           p.KW, glds, acc, tid);
+  gemm_mainloop<SPLIT>(p.a + S.abase, p.a_plane, p.Kp, p.M, m0, S.V, p.KW, S.R, c0, p.Kp / kGK, glds, acc, tid);
 
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  TT* __restrict__ T = static_cast<TT*>(p.t) + S.tbase;
+  uint16_t* __restrict__ T = p.t + S.tbase;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = c0 + 64 * wn + 32 * j + lr;  // < RP; rows R <= r < RP are written as zeros
@@ -773,7 +805,18 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
-        if (m < p.M) store_t(T, int64_t(m) * S.RP + r, lv * acc[i][j][q]);
+        if (m < p.M) {
+          const int64_t o = int64_t(m) * S.RP + r;
+          const float v = lv * acc[i][j][q];
+          if constexpr (SPLIT) {
+            uint16_t h, l;
+            split1(v, h, l);
+            T[o] = h;
+            T[p.t_plane + o] = l;
+          } else {
+            T[o] = f32_to_bf16(v);
+          }
+        }
       }
   }
 }
@@ -781,7 +824,6 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
 // Stage 2.  grid = (m-tiles, column tiles of all projections), 256 threads.
 template <typename YT, bool SPLIT>
 __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
-  using TT = typename std::conditional<SPLIT, float, uint16_t>::type;
   extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
@@ -792,17 +834,17 @@ __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
   const GemmProj& P = p.proj[pi];
   const int m0 = int(blockIdx.x) * kGB;
   const int c0 = (nt - P.nt0) * kGB;
-  const TT* __restrict__ T = static_cast<const TT*>(p.t);
   f32x16 acc0[2][2], acc1[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc0[i][j] = acc1[i][j] = f32x16{};
-  gemm_mainloop<TT, SPLIT>(T + P.tbase[0], P.RP[0], p.M, m0, kGK * P.RW[0], nullptr, true, P.U[0], P.RW[0], P.N, c0,
-                           P.RW[0], glds, acc0, tid);
+  // T rows are zero from R to RP >= 64 * ceil(RW / 2), so whole 64-k steps are safe
+  gemm_mainloop<SPLIT>(p.t + P.tbase[0], p.t_plane, P.RP[0], p.M, m0, P.U[0], P.RW[0], P.N, c0, (P.RW[0] + 1) / 2,
+                       glds, acc0, tid);
   if (P.nb > 1)
-    gemm_mainloop<TT, SPLIT>(T + P.tbase[1], P.RP[1], p.M, m0, kGK * P.RW[1], nullptr, true, P.U[1], P.RW[1], P.N,
-                             c0, P.RW[1], glds, acc1, tid);
+    gemm_mainloop<SPLIT>(p.t + P.tbase[1], p.t_plane, P.RP[1], p.M, m0, P.U[1], P.RW[1], P.N, c0,
+                         (P.RW[1] + 1) / 2, glds, acc1, tid);
 
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -937,12 +979,23 @@ size_t compact_rows(int mt, int64_t nch) {
 
 size_t gemm_lds_bytes(bool split) { return size_t(2) * (split ? 2 : 1) * kGTile * sizeof(uint16_t); }
 
-// T of the GEMM path: per segment [M][RP] (fp32 with SPLIT, else bf16).
-size_t gemm_t_bytes(const ProjDesc* pd, int np, int64_t M, bool split) {
-  size_t n = 0;
+// Elements per plane of the GEMM path's A (per segment [M][Kp]) and T (per
+// segment [M][RP]); planes are bf16, two of each with SPLIT.
+void gemm_planes(const ProjDesc* pd, int np, int64_t M, int64_t K, int64_t& a_plane, int64_t& t_plane) {
+  a_plane = t_plane = 0;
+  const int64_t Kp = ceil_div(K, kGK) * kGK;
   for (int q = 0; q < np; ++q)
-    for (int b = 0; b < pd[q].nb; ++b) n += size_t(M) * size_t(ceil_div(pd[q].br[b].rank, kGB) * kGB);
-  return align256(n * (split ? sizeof(float) : sizeof(uint16_t)));
+    for (int b = 0; b < pd[q].nb; ++b) {
+      a_plane += M * Kp;
+      t_plane += M * ceil_div(pd[q].br[b].rank, kGB) * kGB;
+    }
+}
+
+size_t gemm_ws_bytes(const ProjDesc* pd, int np, int64_t M, int64_t K, bool split) {
+  int64_t ap, tp;
+  gemm_planes(pd, np, M, K, ap, tp);
+  const size_t planes = split ? 2 : 1;
+  return align256(size_t(ap) * planes * sizeof(uint16_t)) + align256(size_t(tp) * planes * sizeof(uint16_t));
 }
 
 Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
@@ -976,7 +1029,7 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     pl.lds2 = lds2;
     pl.ws_total = kTOffset + kTBytes;
   } else {
-    pl.ws_total = kGemmOffset + gemm_t_bytes(pd, np, M, true);
+    pl.ws_total = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
   }
   return pl;
 }
@@ -1106,11 +1159,15 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
+  p.Kp = int(ceil_div(K, kGK) * kGK);
   p.x = x;
-  p.t = static_cast<char*>(workspace) + kGemmOffset;
+  gemm_planes(pd, np, M, K, p.a_plane, p.t_plane);
+  char* ws = static_cast<char*>(workspace) + kGemmOffset;
+  p.a = reinterpret_cast<uint16_t*>(ws);
+  p.t = reinterpret_cast<uint16_t*>(ws + align256(size_t(p.a_plane) * (split ? 2 : 1) * sizeof(uint16_t)));
   bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
   int si = 0, nt1 = 0, nt2 = 0;
-  int64_t tbase = 0;
+  int64_t abase = 0, tbase = 0;
   for (int q = 0; q < np; ++q) {
     GemmProj& P = p.proj[q];
     P.nb = pd[q].nb;
@@ -1128,8 +1185,10 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
       S.R = int(B.rank);
       S.RP = int(ceil_div(B.rank, kGB) * kGB);
       S.nt0 = nt1;
+      S.abase = abase;
       S.tbase = tbase;
       nt1 += S.RP / kGB;
+      abase += M * p.Kp;
       P.U[b] = reinterpret_cast<const uint32_t*>(B.u_sign);
       P.h[b] = B.u1;
       P.RW[b] = int(ceil_div(B.rank, 32));
@@ -1144,10 +1203,15 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
   const int64_t mtiles = ceil_div(M, kGB);
   if (nt1 > 65535 || nt2 > 65535) return set_error(LBK_ERR_ARG, "too many column tiles for the GEMM path");
   const size_t lds = gemm_lds_bytes(split);
+  const dim3 g0{unsigned(M), unsigned(si), 1u};
   const dim3 g1{unsigned(mtiles), unsigned(nt1), 1u}, g2{unsigned(mtiles), unsigned(nt2), 1u};
-  if (split) hipLaunchKernelGGL((gemm_latent_kernel<float, true>), g1, dim3(kGThreads), lds, s, p);
-  else hipLaunchKernelGGL((gemm_latent_kernel<uint16_t, false>), g1, dim3(kGThreads), lds, s, p);
-  int rc = check_launch("gemm_latent_kernel");
+  if (x_dtype == LBK_F32) hipLaunchKernelGGL((gemm_scale_kernel<float, true>), g0, dim3(kGThreads), 0, s, p);
+  else hipLaunchKernelGGL((gemm_scale_kernel<uint16_t, false>), g0, dim3(kGThreads), 0, s, p);
+  int rc = check_launch("gemm_scale_kernel");
+  if (rc != LBK_OK) return rc;
+  if (split) hipLaunchKernelGGL((gemm_latent_kernel<true>), g1, dim3(kGThreads), lds, s, p);
+  else hipLaunchKernelGGL((gemm_latent_kernel<false>), g1, dim3(kGThreads), lds, s, p);
+  rc = check_launch("gemm_latent_kernel");
   if (rc != LBK_OK) return rc;
   if (split) {
     if (y_dtype == LBK_F32) hipLaunchKernelGGL((gemm_expand_kernel<float, true>), g2, dim3(kGThreads), lds, s, p);
