@@ -26,6 +26,7 @@ __all__ = [
     "config_seed",
     "LLAMA2_7B",
     "llama_projection_shapes",
+    "synthetic_runtime_state",
 ]
 
 
@@ -130,3 +131,65 @@ def llama_projection_shapes(cfg: Optional[Dict] = None, residual: bool = False):
     ):
         out.append((name, K, N, [r, rr] if residual else [r]))
     return out
+
+
+def synthetic_runtime_state(config, draft_ranks: Dict[str, int], residual_ranks: Optional[Dict[str, int]] = None,
+                            seed: int = 0, device="cpu", normalized: bool = False, embed: bool = True):
+    """A runtime-layout state dict (convert_hf_to_runtime.py key names) of a
+    random LittleBit Llama model: packed sign words, scales |N(0,1)| + 0.05,
+    norm weights 1 + 0.1 N(0,1), and (``embed``) ``model.embed_tokens.weight``
+    and ``lm_head.weight`` ~ N(0, 1).
+
+    ``draft_ranks`` / ``residual_ranks`` map "attn" / "mlp" to ranks;
+    ``residual_ranks`` adds in-module residual branches (``_r`` keys).
+    ``normalized`` divides g by sqrt(K) and l by sqrt(R) so that every
+    projection maps unit-RMS inputs to O(1) outputs (keeps attention scores
+    moderate for numerical comparisons); the benchmark leaves it off.
+    """
+    import torch
+
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(int(seed))
+    c = config
+    kv = c.num_key_value_heads * c.head_dim
+    shapes = {"self_attn.q_proj": (c.hidden_size, c.hidden_size, "attn"),
+              "self_attn.k_proj": (c.hidden_size, kv, "attn"),
+              "self_attn.v_proj": (c.hidden_size, kv, "attn"),
+              "self_attn.o_proj": (c.hidden_size, c.hidden_size, "attn"),
+              "mlp.gate_proj": (c.hidden_size, c.intermediate_size, "mlp"),
+              "mlp.up_proj": (c.hidden_size, c.intermediate_size, "mlp"),
+              "mlp.down_proj": (c.intermediate_size, c.hidden_size, "mlp")}
+
+    def words(rows, cols):
+        wpr = (cols + 31) // 32
+        w = torch.randint(-2**31, 2**31, (rows, wpr), generator=gen, dtype=torch.int64, device=dev)
+        tail = cols - 32 * (wpr - 1)
+        if tail < 32:
+            w[:, -1] &= (1 << tail) - 1
+        return w.to(torch.int32)
+
+    def scales(n, div=1.0):
+        return ((torch.randn(n, generator=gen, device=dev).abs() + 0.05) / div).reshape(1, n)
+
+    state = {}
+    for i in range(c.num_hidden_layers):
+        for name, (K, N, kind) in shapes.items():
+            p = f"model.layers.{i}.{name}"
+            for tag, sfx, ranks in (("", "", draft_ranks), ("_r", "_r", residual_ranks)):
+                if ranks is None:
+                    continue
+                R = int(ranks[kind])
+                state[f"{p}.v_sign{tag}_rt"] = words(R, K)
+                state[f"{p}.v_sign{tag}_rt_shape"] = torch.tensor([R, K], dtype=torch.int64)
+                state[f"{p}.u_sign{tag}_rt"] = words(N, R)
+                state[f"{p}.u_sign{tag}_rt_shape"] = torch.tensor([N, R], dtype=torch.int64)
+                state[f"{p}.v2{sfx}"] = scales(K, K ** 0.5 if normalized else 1.0)
+                state[f"{p}.mid{sfx}"] = scales(R, R ** 0.5 if normalized else 1.0)
+                state[f"{p}.u1{sfx}"] = scales(N)
+        for nm in ("input_layernorm", "post_attention_layernorm"):
+            state[f"model.layers.{i}.{nm}.weight"] = 1 + 0.1 * torch.randn(c.hidden_size, generator=gen, device=dev)
+    state["model.norm.weight"] = 1 + 0.1 * torch.randn(c.hidden_size, generator=gen, device=dev)
+    if embed:
+        state["model.embed_tokens.weight"] = torch.randn((c.vocab_size, c.hidden_size), generator=gen, device=dev)
+        state["lm_head.weight"] = torch.randn((c.vocab_size, c.hidden_size), generator=gen, device=dev)
+    return state

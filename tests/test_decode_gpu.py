@@ -1,0 +1,213 @@
+"""GPU decode/verify steps (the call sites of the forward) against a float64
+reference decoder built on the oracle, and the speculative loops against
+the target's own greedy decoding.
+
+The reference decoder restates the layer of full_forward_cpu
+(patches/littlebit_cpu_optimized.cpp:1522-1840): RMSNorm, q/k/v, GQA
+attention without rotary embedding over the cache, o + residual, RMSNorm,
+SiLU(gate) * up, down + residual, final RMSNorm; its projections are
+oracle.littlebit_forward on the same packed words.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import littlebit_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _cfg():
+    from littlebit_amd.decode import DecoderConfig
+    return DecoderConfig(hidden_size=128, intermediate_size=320, num_hidden_layers=2, num_attention_heads=4,
+                         num_key_value_heads=2, vocab_size=384, rms_norm_eps=1e-6)
+
+
+def _state(seed, residual=True, draft=(16, 24), res=(40, 56)):
+    from littlebit_amd.synthetic import synthetic_runtime_state
+    return synthetic_runtime_state(_cfg(), {"attn": draft[0], "mlp": draft[1]},
+                                   {"attn": res[0], "mlp": res[1]} if residual else None,
+                                   seed=seed, normalized=True)
+
+
+def _np(t):
+    return t.detach().cpu().double().numpy()
+
+
+def _branches(state, p, residual):
+    out = []
+    for tag, sfx in (("", ""), ("_r", "_r")):
+        if f"{p}.u_sign{tag}_rt" not in state or (tag and not residual):
+            continue
+        v = state[f"{p}.v_sign{tag}_rt"].numpy()
+        out.append({"v_sign": v, "u_sign": state[f"{p}.u_sign{tag}_rt"].numpy(),
+                    "g": _np(state[f"{p}.v2{sfx}"]).reshape(-1), "l": _np(state[f"{p}.mid{sfx}"]).reshape(-1),
+                    "h": _np(state[f"{p}.u1{sfx}"]).reshape(-1), "R": v.shape[0]})
+    return out
+
+
+def ref_hidden(state, cfg, ids, residual):
+    """Final-norm hidden [N, H] of tokens ids[0..N) from an empty cache."""
+    H, eps = cfg.hidden_size, cfg.rms_norm_eps
+    kvh, hd, rep = cfg.num_key_value_heads, cfg.head_dim, cfg.kv_repeat
+
+    def norm(x, w):
+        return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+
+    def lin(x, p, K, N):
+        return O.littlebit_forward(x, _branches(state, p, residual), K, N)
+
+    x = _np(state["model.embed_tokens.weight"])[ids]
+    n = len(ids)
+    for i in range(cfg.num_hidden_layers):
+        p = f"model.layers.{i}"
+        h = norm(x, _np(state[f"{p}.input_layernorm.weight"]))
+        q = lin(h, f"{p}.self_attn.q_proj", H, H).reshape(n, kvh, rep, hd)
+        k = lin(h, f"{p}.self_attn.k_proj", H, kvh * hd).reshape(n, kvh, hd)
+        v = lin(h, f"{p}.self_attn.v_proj", H, kvh * hd).reshape(n, kvh, hd)
+        s = np.einsum("tgrd,sgd->grts", q, k) * cfg.attn_scale
+        s = np.where(np.tril(np.ones((n, n), bool))[None, None], s, -np.inf)
+        s = np.exp(s - s.max(-1, keepdims=True))
+        s /= s.sum(-1, keepdims=True)
+        a = np.einsum("grts,sgd->tgrd", s, v).reshape(n, H)
+        x = x + lin(a, f"{p}.self_attn.o_proj", H, H)
+        h = norm(x, _np(state[f"{p}.post_attention_layernorm.weight"]))
+        I = cfg.intermediate_size
+        g = lin(h, f"{p}.mlp.gate_proj", H, I)
+        u = lin(h, f"{p}.mlp.up_proj", H, I)
+        x = x + lin(g / (1 + np.exp(-g)) * u, f"{p}.mlp.down_proj", I, H)
+    return norm(x, _np(state["model.norm.weight"]))
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_decoder_matches_float64_reference(gpu, residual):
+    from littlebit_amd.decode import LittleBitDecoder
+    cfg = _cfg()
+    st = _state(11)
+    dec = LittleBitDecoder(st, cfg, gpu, max_seq_len=64, residual=None if residual else False)
+    ids = [3, 17, 250, 9, 101, 42, 7]
+    h = dec.forward_batch(ids, st["model.embed_tokens.weight"].to(gpu))
+    err = O.rel_err(h.cpu().numpy(), ref_hidden(st, cfg, ids, residual))
+    print(f"[decode] residual={residual} rel_err={err:.2e}", flush=True)
+    assert err <= TOL
+
+
+def test_batch_equals_token_by_token(gpu):
+    from littlebit_amd.decode import LittleBitDecoder
+    cfg = _cfg()
+    st = _state(12)
+    emb = st["model.embed_tokens.weight"].to(gpu)
+    ids = [5, 6, 7, 8, 300, 2]
+    a = LittleBitDecoder(st, cfg, gpu, max_seq_len=32)
+    b = LittleBitDecoder(st, cfg, gpu, max_seq_len=32)
+    hb = a.forward_batch(ids, emb)
+    ht = torch.cat([b.forward_token(t, emb) for t in ids])
+    assert O.rel_err(hb.cpu().numpy(), ht.cpu().numpy()) <= 1e-5
+    assert a.cache_pos == b.cache_pos == len(ids)
+
+
+def test_draft_graph_equals_eager_and_rolls_back(gpu):
+    from littlebit_amd.decode import GPUDraftModel
+    cfg = _cfg()
+    st = _state(13, residual=False)
+    g = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=True)
+    e = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False)
+    prompt = torch.tensor([[1, 44, 90, 200, 3]])
+    for rnd in range(3):
+        tg, pg = g.generate_draft_tokens(prompt, draft_length=6)
+        te, pe = e.generate_draft_tokens(prompt, draft_length=6)
+        assert [int(t) for t in tg] == [int(t) for t in te], f"round {rnd}"
+        for a, b in zip(pg, pe):
+            assert a.shape == (1, 1, cfg.vocab_size)
+            assert float((a - b).abs().max()) <= 1e-4
+        assert g._cache_pos == prompt.shape[1] and g._cached_seq_len == prompt.shape[1]
+        # next prompt = accepted drafts + one more token: only the new part is computed
+        prompt = torch.cat([prompt, torch.tensor([[int(tg[0]), int(tg[1]), 77]])], dim=1)
+    # a fresh model on the final prompt drafts the same tokens
+    f = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False)
+    assert [int(t) for t in f.generate_draft_tokens(prompt, draft_length=4)[0]] == \
+           [int(t) for t in g.generate_draft_tokens(prompt, draft_length=4)[0]]
+
+
+def test_target_prefix_reuse_and_zero_rows(gpu):
+    from littlebit_amd.decode import GPUTargetModel
+    cfg = _cfg()
+    d, r = _state(14, residual=False), _state(15, residual=False)
+    t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=64)
+    fresh = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=64)
+    a = torch.tensor([[4, 8, 15, 16, 23]])
+    b = torch.tensor([[4, 8, 15, 99, 42, 7]])  # shares 3 tokens
+    t.forward(a)
+    lb = t.forward(b)
+    assert float(lb[0, :3].abs().max()) == 0.0
+    full = fresh.forward(b)
+    assert O.rel_err(lb[0, 3:].cpu().numpy(), full[0, 3:].cpu().numpy()) <= 1e-5
+    # hidden sum of two units = logits through one lm_head (cpu_target_model.py:520-527)
+    # both units embed with the draft checkpoint's table, as with the shared base model
+    r_shared = {**r, "model.embed_tokens.weight": d["model.embed_tokens.weight"]}
+    h = ref_hidden(d, cfg, b[0].tolist(), False) + ref_hidden(r_shared, cfg, b[0].tolist(), False)
+    W = d["lm_head.weight"].double().numpy()
+    assert O.rel_err(full[0].cpu().numpy(), h @ W.T) <= TOL
+
+
+def test_single_unit_target_uses_residual_branches(gpu):
+    from littlebit_amd.decode import GPUTargetModel
+    cfg = _cfg()
+    st = _state(16, residual=True)
+    t = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
+    ids = [1, 2, 3, 4]
+    lg = t.forward(torch.tensor([ids]))
+    ref = ref_hidden(st, cfg, ids, True) @ st["lm_head.weight"].double().numpy().T
+    assert O.rel_err(lg[0].cpu().numpy(), ref) <= TOL
+
+
+def test_forward_tree_chain_equals_sequence(gpu):
+    """A tree that is one chain verifies like the plain sequence."""
+    from littlebit_amd.decode import GPUTargetModel
+    from littlebit_amd.tree import generate_tree_buffers
+    cfg = _cfg()
+    st = _state(17)
+    t1 = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
+    t2 = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
+    prefix = [9, 8, 7, 6]
+    chain = [31, 32, 33]
+    bufs = generate_tree_buffers([[0], [0, 0], [0, 0, 0]], device=gpu)
+    lt = t1.forward_tree(torch.tensor([prefix]), [prefix[-1]] + chain, bufs["tree_attn_mask"][0, 0])
+    ls = t2.forward(torch.tensor([prefix + chain]))
+    assert O.rel_err(lt.cpu().numpy(), ls[0, len(prefix) - 1:].cpu().numpy()) <= 1e-5
+    assert t1.draft_unit.cache_pos == len(prefix)
+
+
+def test_speculative_greedy_equals_autoregressive(gpu):
+    from littlebit_amd.decode import GPUDraftModel, GPUTargetModel
+    from littlebit_amd.speculative import autoregressive_decode, speculative_decode
+    cfg = _cfg()
+    d, r = _state(18, residual=False), _state(19, residual=False)
+    draft = GPUDraftModel(state=d, config=cfg, device=gpu, max_seq_len=96)
+    target = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=96)
+    ref_t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=96)
+    prompt = torch.tensor([[10, 20, 30, 40]])
+    out, stats = speculative_decode(draft, target, prompt, max_new_tokens=24, draft_length=5, eos_token_id=-1)
+    ref = autoregressive_decode(ref_t, prompt, 24, eos_token_id=-1)
+    print(f"[spec] accepted {stats['total_accepted_tokens']}/{stats['total_draft_tokens']}", flush=True)
+    assert out.tolist() == ref.tolist()
+    assert stats["total_tokens_generated"] == 24
+
+
+def test_speculative_tree_equals_autoregressive(gpu):
+    from littlebit_amd.decode import GPUDraftModel, GPUTargetModel
+    from littlebit_amd.speculative import autoregressive_decode, speculative_decode_tree
+    from littlebit_amd.tree import generate_tree_buffers, ranked_tree_choices
+    cfg = _cfg()
+    d, r = _state(20, residual=False), _state(21, residual=False)
+    draft = GPUDraftModel(state=d, config=cfg, device=gpu, max_seq_len=128, use_graph=False)
+    target = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=128)
+    ref_t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=128)
+    bufs = generate_tree_buffers(ranked_tree_choices(12, 4, 3), device=gpu)
+    prompt = torch.tensor([[3, 1, 4, 1, 5]])
+    out, stats = speculative_decode_tree(draft, target, prompt, max_new_tokens=16, tree_buffers=bufs, top_k=4,
+                                         eos_token_id=-1)
+    ref = autoregressive_decode(ref_t, prompt, 16, eos_token_id=-1)
+    assert out.tolist() == ref.tolist()
