@@ -37,6 +37,11 @@ if str(ROOT) not in sys.path:
 
 METRIC = "µs/layer + achieved GB/s (LittleBitLinear GEMV); draft tok/s, Llama-2-7B 0.1BPW"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per call of a call kind's kernel pair, from two rocprofv3 --pmc passes
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a 256 MiB device copy reads);
+# commands and figures in profiles/littlebit_decode_calls.md.  Measured for the
+# current kernels; a kind without a measurement reports null.
+MEASURED_TRAFFIC = {"down": 1_400_300}
 MALL_BYTES = 256 << 20
 
 
@@ -81,22 +86,23 @@ class Call:
     """One launch pair: a projection or a group of projections with a shared
     input, its input x [1, K] and outputs."""
 
-    def __init__(self, gen, dev, names, grouped=True):
+    def __init__(self, gen, dev, names, grouped=True, M=1, residual=False):
         import torch
         from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
-        shapes = {s[0]: s for s in draft_layer_shapes()}
+        from littlebit_amd.synthetic import llama_projection_shapes
+        shapes = {s[0]: s for s in llama_projection_shapes(residual=residual)}
         self.names = names
         self.projs = []
         for nm in names:
             _, K, N, ranks = shapes[nm]
             self.projs.append(LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks]))
         self.K = self.projs[0].in_features
-        self.x = torch.randn((1, self.K), generator=gen).to(dev)
-        self.outs = [torch.empty((1, p.out_features), device=dev) for p in self.projs]
+        self.x = torch.randn((M, self.K), generator=gen).to(dev)
+        self.outs = [torch.empty((M, p.out_features), device=dev) for p in self.projs]
         self.group = LittleBitProjectionGroup(self.projs) if grouped and len(self.projs) > 1 else None
-        self.bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks) for p in self.projs)
-        self.weight_bytes = sum(proj_bytes(1, p.in_features, p.out_features, p.ranks)
-                                - 4 * (p.in_features + p.out_features) for p in self.projs)
+        self.bytes = sum(proj_bytes(M, p.in_features, p.out_features, p.ranks) for p in self.projs)
+        self.weight_bytes = sum(proj_bytes(M, p.in_features, p.out_features, p.ranks)
+                                - 4 * M * (p.in_features + p.out_features) for p in self.projs)
 
     def run(self):
         if self.group is not None:
@@ -109,8 +115,8 @@ class Call:
 class DraftStep:
     """One replica of a step's 224 projections (32 layers x 7) as calls."""
 
-    def __init__(self, gen, dev, layers, grouped=True):
-        self.calls = [Call(gen, dev, names, grouped) for _ in range(layers) for _, names in LAYER_CALLS]
+    def __init__(self, gen, dev, layers, grouped=True, M=1, residual=False):
+        self.calls = [Call(gen, dev, names, grouped, M, residual) for _ in range(layers) for _, names in LAYER_CALLS]
 
     @property
     def bytes(self):
@@ -216,6 +222,103 @@ def prefill_bench(gen, dev, stream, steps=20, warmup=3):
             "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "us_per_call": per_call}
 
 
+def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5):
+    """Config 3's verify linears: the 224 target projections (draft + residual
+    branch each) at M = 8, grouped as in the draft step, one HIP graph per
+    pass, weights cold (2 replicas of 0.9 GB rotated)."""
+    import torch
+    reps = [DraftStep(gen, dev, layers, M=M, residual=True) for _ in range(2)]
+    graphs = [capture(r.run, stream) for r in reps]
+    ms = time_graphs(graphs, steps, warmup, stream)
+    b = reps[0].bytes
+    gbs = b / (ms * 1e-3) / 1e9
+    return {"workload": f"llama2-7b 1.0-bpw target linears, {layers} layers x 7 projections at M={M} "
+                        "(draft rank 205/298 + residual 1843/2686 per projection), fp32",
+            "ms_per_pass": round(ms, 4), "us_per_layer": round(ms * 1000.0 / layers, 2),
+            "bytes_per_pass": b, "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32):
+    """Config 2 draft tokens and config 3 verification on whole Llama-2-7B-shaped
+    models (random packed factors, |N|+0.05 scales; embedding and a bf16
+    lm_head N(0,1)): attention, norms and lm_head in PyTorch, linears on the
+    HIP kernels."""
+    import torch
+    from littlebit_amd.decode import DecoderConfig, GPUDraftModel, GPUTargetModel
+    from littlebit_amd.synthetic import LLAMA2_7B as C, synthetic_runtime_state
+    from littlebit_amd.tree import config3_tree_choices, generate_tree_buffers
+    cfg = DecoderConfig(hidden_size=C["hidden"], intermediate_size=C["intermediate"], num_hidden_layers=C["layers"],
+                        num_attention_heads=C["heads"], num_key_value_heads=C["kv_heads"], vocab_size=C["vocab"])
+    ev = lambda: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))  # noqa: E731
+    out = {}
+    gen = torch.Generator().manual_seed(5)
+    # --- config 2: draft model, KV length 512 -------------------------------------
+    st = synthetic_runtime_state(cfg, C["draft_rank"], None, seed=1, device=dev)
+    draft = GPUDraftModel(state=st, config=cfg, device=dev, max_seq_len=kv_draft + replays + draft_len + 8,
+                          torch_dtype=torch.bfloat16)
+    prompt = torch.randint(0, cfg.vocab_size, (1, kv_draft), generator=gen)
+    draft.generate_draft_tokens(prompt, draft_length=2)  # prefill + builds the graph
+    torch.cuda.synchronize()
+    draft._pos.fill_(kv_draft)
+    for _ in range(3):
+        draft._graph.replay()
+    draft._pos.fill_(kv_draft)
+    a, b = ev()
+    a.record()
+    for _ in range(replays):
+        draft._graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms_tok = a.elapsed_time(b) / replays
+    a, b = ev()
+    a.record()
+    draft.generate_draft_tokens(prompt, draft_length=draft_len)
+    b.record()
+    torch.cuda.synchronize()
+    out["draft"] = {"workload": f"llama2-7b 0.1-bpw draft, one token at KV length {kv_draft}: embedding, 32 layers "
+                                "(norms, attention, 7 LittleBitLinear forwards), final norm, bf16 lm_head, argmax; "
+                                "one HIP graph per token",
+                    "ms_per_token": round(ms_tok, 4), "tok_per_s": round(1000.0 / ms_tok, 1),
+                    f"generate_draft_tokens_k{draft_len}_ms": round(a.elapsed_time(b), 3)}
+    del draft, st
+    torch.cuda.empty_cache()
+    # --- config 3: 1.0-BPW target (draft + residual branch per projection), KV length 1024
+    st = synthetic_runtime_state(cfg, C["draft_rank"], C["residual_rank"], seed=2, device=dev)
+    target = GPUTargetModel(draft_state=st, config=cfg, device=dev, max_seq_len=kv_target + 64,
+                            torch_dtype=torch.bfloat16)
+    prefix = torch.randint(0, cfg.vocab_size, (1, kv_target), generator=gen)
+    target.forward(prefix)
+    toks = torch.randint(0, cfg.vocab_size, (1, draft_len), generator=gen)
+
+    import torch.nn.functional as F
+    from littlebit_amd.synthetic import llama_projection_shapes
+    unit, W = target.draft_unit, target.lm_head_weight
+    stream = torch.cuda.Stream()
+    bufs = generate_tree_buffers(config3_tree_choices(), device=dev)
+    tree = [int(prefix[0, -1])] + torch.randint(0, cfg.vocab_size, (bufs["tree_len"] - 1,), generator=gen).tolist()
+    x_v = target.embed_tokens.index_select(0, toks[0].to(dev))
+    x_t = target.embed_tokens.index_select(0, torch.tensor(tree, device=dev))
+    tmask = bufs["tree_attn_mask"][0, 0].bool()
+
+    def vstep():  # the draft_len new tokens after the prefix, causal
+        F.linear(unit.forward_hidden(x_v, kv_target).to(W.dtype), W)
+
+    def tstep():  # root (last prefix token) + tree nodes, ancestor mask
+        F.linear(unit.forward_hidden(x_t, kv_target - 1, tree_mask=tmask).to(W.dtype), W)
+
+    ms_v = time_graphs([capture(vstep, stream)], 20, 3, stream)
+    ms_t = time_graphs([capture(tstep, stream)], 20, 3, stream)
+    vbytes = 32 * sum(proj_bytes(draft_len, K, N, ranks) for _, K, N, ranks in llama_projection_shapes(residual=True))
+    out["verify"] = {"workload": f"llama2-7b 1.0-bpw target (draft + residual branch per projection) at KV length "
+                                 f"{kv_target}: {draft_len} tokens in one forward, and a {bufs['tree_len'] - 1}-node "
+                                 "tree (depth 5, branching <= 4) plus its root in one forward with the tree mask; "
+                                 "each one HIP graph (32 layers, attention, norms, bf16 lm_head)",
+                     f"verify_{draft_len}_ms": round(ms_v, 4), "tree_verify_ms": round(ms_t, 4),
+                     f"linear_bytes_per_verify": vbytes,
+                     f"round_ms_k{draft_len}": round(draft_len * ms_tok + ms_v, 3)}
+    return out
+
+
 def cpu_baseline(layers, budget_s=12.0):
     """The reference littlebit_linear (int8-quantised AVX2) over whole draft
     steps on the host cores, within a time budget."""
@@ -269,7 +372,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
-    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill"], default=None,
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
+    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "verify", "copy"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -288,6 +392,23 @@ def main():
     kinds = dict(LAYER_CALLS)
     if args.only == "prefill":
         print(json.dumps(prefill_bench(gen, dev, stream, args.steps, args.warmup)))
+        return
+    if args.only == "copy":
+        # calibration for the HBM byte counters: a plain device copy of known size
+        n = 64 << 20  # floats: 256 MiB read + 256 MiB written per copy
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_read_per_copy": 4 * n, "bytes_written_per_copy": 4 * n,
+                          "copies": max(args.steps, 1)}))
+        return
+    if args.only == "decode":
+        print(json.dumps(decode_bench(dev)))
+        return
+    if args.only == "verify":
+        print(json.dumps(verify_linears_bench(gen, dev, stream, args.layers, steps=args.steps, warmup=args.warmup)))
         return
     if args.only:
         names = kinds[args.only.replace("gate_up", "gate/up")]
@@ -318,11 +439,13 @@ def main():
     dom = max(cls_stats, key=lambda c: cls_stats[c]["us_per_call"])
     d = cls_stats[dom]
     roofline = {"bound": "hbm", "achieved": round(d["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": None,
+                "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC.get(dom),
                 "kernel": f"LittleBitLinear {dom} call ({d['projections']}): latent_mfma_kernel + expand_mfma_kernel",
                 "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_call"]}
 
+    verify_lin = verify_linears_bench(gen, dev, stream, args.layers)
     prefill = None if args.no_prefill else prefill_bench(gen, dev, stream)
+    decode = None if args.no_decode else decode_bench(dev)
     cpu = None if args.no_cpu else cpu_baseline(args.layers, args.cpu_budget)
     value = step_bytes / (ms_cold * 1e-3) / 1e9
     out = {
@@ -354,7 +477,9 @@ def main():
         "per_class": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in cls_stats.items()},
         "roofline": roofline,
+        "verify_linears": verify_lin,
         "prefill": prefill,
+        "decode": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

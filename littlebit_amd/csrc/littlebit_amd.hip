@@ -223,6 +223,18 @@ struct Compact {
   }
 };
 
+// Blocks are dispatched to the 8 XCDs of MI355X round-robin (block b runs on
+// XCD b % 8, confirmed on the device).  This maps block b to a logical index
+// so that each XCD gets one contiguous range of logical blocks: neighbouring
+// k-chunks of a row-block, which share 128-byte lines of the sign rows, then
+// meet in one L2 instead of fetching the line from HBM once per XCD.  Any
+// other dispatch order only changes the traffic, not the result.
+__device__ __forceinline__ int xcd_contiguous_block(int b, int G) {
+  const int x = b & 7, j = b >> 3;
+  const int q = G >> 3, r = G & 7;  // XCD x holds q + (x < r) blocks
+  return x * q + min(x, r) + j;
+}
+
 // Fill a compact operand: one thread per chunk; load_row(c, m, a) gives the
 // 8 values of chunk c for m < M.  All loads of a block are issued before any
 // is used; rows m >= M are written as zeros (their loads read row M - 1).
@@ -267,8 +279,9 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   constexpr int KC = 128 * WPL;
   constexpr int NCH = KC / 8;  // 8-column chunks per k-chunk
 
-  const int rbk = int(blockIdx.x) / p.nkc;
-  const int kc = int(blockIdx.x) - rbk * p.nkc;
+  const int lb = xcd_contiguous_block(int(blockIdx.x), int(gridDim.x));
+  const int rbk = lb / p.nkc;
+  const int kc = lb - rbk * p.nkc;
   // segment of this row-block: a wave-uniform index, so the descriptor is
   // read with scalar loads from the kernel arguments
   int si = 0;

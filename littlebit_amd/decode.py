@@ -297,6 +297,7 @@ class GPUDraftModel:
         self._cache_pos = 0
         self._cached_seq_len = 0
         self._last_hidden = None
+        self._prompt_hidden = None
         self.use_graph = bool(use_graph)
         self._graph = None
 
@@ -305,6 +306,7 @@ class GPUDraftModel:
         self._cache_pos = 0
         self._cached_seq_len = 0
         self._last_hidden = None
+        self._prompt_hidden = None  # final hidden of the last cached prompt token
 
     def _lm_head(self, hidden: torch.Tensor) -> torch.Tensor:
         return F.linear(hidden.to(self.lm_head_weight.dtype), self.lm_head_weight).to(torch.float32)
@@ -355,12 +357,12 @@ class GPUDraftModel:
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor):
         """Cache the prompt's KV; only positions not yet cached are computed
-        (cpu_draft_model.py:437-461)."""
+        (cpu_draft_model.py:437-461).  A prompt that repeats the cached one
+        is not recomputed (the reference's Python path resets then, its C++
+        path does not); a shorter prompt resets the cache."""
         seq_len = int(input_ids.shape[1])
-        if self._cached_seq_len > 0 and seq_len > self._cached_seq_len:
-            start = self._cached_seq_len
-        elif self._cached_seq_len == 0:
-            start = 0
+        if self._cached_seq_len > 0 and seq_len >= self._cached_seq_len and self._prompt_hidden is not None:
+            start = self._cached_seq_len  # extends (or repeats) the cached prompt
         else:
             self.reset()
             start = 0
@@ -368,8 +370,9 @@ class GPUDraftModel:
         if ids:
             self.unit.cache_pos = start
             h = self.unit.forward_batch(ids, self.embed_tokens)
-            self._last_hidden = h[-1:]
-            self._cache_pos = start + len(ids)
+            self._prompt_hidden = h[-1:]
+        self._last_hidden = self._prompt_hidden
+        self._cache_pos = seq_len
         self._cached_seq_len = seq_len
 
     @torch.no_grad()
@@ -418,6 +421,7 @@ class GPUDraftModel:
                     last_hidden = self._forward_token(int(nxt.item()))
         self._cache_pos = cache_pos_before_draft
         self._cached_seq_len = seq_len
+        self._last_hidden = self._prompt_hidden
         return tokens, probs
 
 
