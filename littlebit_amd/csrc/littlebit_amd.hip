@@ -38,6 +38,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "littlebit_amd.h"
@@ -58,7 +60,8 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int64_t kMaxDim = int64_t(1) << 24;  // K, N, M limit
 constexpr int64_t kMaxRankTotal = 16384;       // sum of branch ranks
-constexpr int kMaxLds = 159 * 1024;            // gfx950: 160 KB per workgroup, 1 KB kept for static LDS
+constexpr int kLdsPerCU = 160 * 1024;          // gfx950: LDS per CU
+constexpr int kMaxBlockLds = 159 * 1024;       // static + dynamic LDS of one block (a 160 KB request failed to launch)
 constexpr int kRowBlock = 64;                  // latent rows per latent_mfma block
 constexpr int kMaxMfmaM = 16;                  // MFMA path handles M <= 16
 constexpr int kCounterSlots = 1024;            // counters at the workspace start
@@ -405,22 +408,23 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 // block = 2 * TILES waves covering 16 * TILES output rows of one projection:
 // wave w owns tile w % TILES (16 rows) and half w / TILES of the rank steps
 // (4 sign words of a row) of both branches; the two halves meet in LDS.
-// Every block reads all of its projection's t, so larger M (a larger
-// operand) takes more rows per block.
+// Every block stages all of its projection's t, so the host picks TILES (2,
+// 4 or 8) to need the fewest rounds of blocks on the CUs that the LDS size
+// allows, then the fewest staging passes, then the most blocks.
 // grid.x = sum over projections of ceil(N / (16 * TILES))
 // LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
 // ---------------------------------------------------------------------------
-template <int MT>
+template <int TILES_>
 struct ExpandShape {
-  static constexpr int TILES = MT >= 4 ? 4 : 2;
+  static constexpr int TILES = TILES_;
   static constexpr int THREADS = 2 * TILES * kWave;
   static constexpr int ROWS = 16 * TILES;
 };
 
-template <typename YT, int MT, int S>
-__global__ __launch_bounds__(ExpandShape<MT>::THREADS) void expand_mfma_kernel(MfmaParams p) {
+template <typename YT, int MT, int S, int TILES>
+__global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kernel(MfmaParams p) {
   using L = Compact<MT>;
-  using E = ExpandShape<MT>;
+  using E = ExpandShape<TILES>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   u32x4* lds_t = reinterpret_cast<u32x4*>(lds_raw);
   __shared__ float red[E::TILES][L::MB * 4][32];
@@ -978,6 +982,7 @@ struct Plan {
   int nkc;       // k-chunks
   int nrb;       // row-blocks over all segments
   int wsteps;    // expand_mfma_kernel unroll bound S
+  int tiles;     // expand_mfma_kernel 16-row tiles per block
   size_t lds1, lds2;
   size_t ws_total;
 };
@@ -1011,9 +1016,37 @@ size_t gemm_ws_bytes(const ProjDesc* pd, int np, int64_t M, int64_t K, bool spli
   return align256(size_t(ap) * planes * sizeof(uint16_t)) + align256(size_t(tp) * planes * sizeof(uint16_t));
 }
 
+// Static LDS of expand_mfma_kernel (the `red` array).
+size_t expand_static_lds(int tiles, int mt) { return size_t(tiles) * ((mt + 7) / 8) * 4 * 32 * sizeof(float); }
+
+// Rows per expand block: fewest rounds of blocks on 256 CUs (blocks per CU
+// bounded by LDS and by 2048 threads), then fewest passes of the t staging
+// loop (chunks per thread), then the most blocks.  0 if no shape fits in
+// the 160 KB of LDS.
+int expand_tiles(const ProjDesc* pd, int np, int mt, size_t lds2, int64_t chunks) {
+  constexpr int kCUs = 256;
+  int best = 0;
+  int64_t best_key[3] = {INT64_MAX, INT64_MAX, INT64_MAX};
+  for (int t : {2, 4, 8}) {
+    if (t == 8 && mt < 4) continue;
+    const int threads = 2 * t * kWave;
+    const size_t lds = lds2 + expand_static_lds(t, mt);
+    if (lds > size_t(kMaxBlockLds)) continue;
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(int64_t(kLdsPerCU) / int64_t(lds), 2048 / threads));
+    int64_t blocks = 0;
+    for (int q = 0; q < np; ++q) blocks += ceil_div(pd[q].N, 16 * t);
+    const int64_t key[3] = {ceil_div(blocks, kCUs * per_cu), ceil_div(chunks, threads), -blocks};
+    if (std::lexicographical_compare(key, key + 3, best_key, best_key + 3)) {
+      best = t;
+      std::copy(key, key + 3, best_key);
+    }
+  }
+  return best;
+}
+
 Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   Plan pl{};
-  int64_t nrb = 0, steps_max = 0;
+  int64_t nrb = 0, steps_max = 0, chunks_max = 0;
   size_t lds2 = 0;
   pl.mt = mtile(M);
   for (int q = 0; q < np; ++q) {
@@ -1024,12 +1057,14 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
       nrb += ceil_div(R, kRowBlock);
     }
     const size_t l2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
+    if (4 * rwp_sum > chunks_max) chunks_max = 4 * rwp_sum;
     if (l2 > lds2) lds2 = l2;
     const int64_t ws = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
     if (ws > steps_max) steps_max = ws;
   }
   pl.nrb = int(nrb);
-  pl.mfma = (M >= 1 && M <= kMaxMfmaM && lds2 <= size_t(kMaxLds) && steps_max <= kMaxWaveSteps);
+  pl.mfma = (M >= 1 && M <= kMaxMfmaM && steps_max <= kMaxWaveSteps &&
+             expand_tiles(pd, np, pl.mt, lds2, chunks_max) > 0);
   if (pl.mfma) {
     // enough blocks to cover the CUs, short per-wave chains
     pl.wpl = 2;
@@ -1040,6 +1075,7 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     pl.wsteps = steps_max <= 4 ? 4 : steps_max <= 8 ? 8 : steps_max <= 16 ? 16 : 24;
     pl.lds1 = compact_rows(pl.mt, 128 * pl.wpl / 8) * 16;
     pl.lds2 = lds2;
+    pl.tiles = expand_tiles(pd, np, pl.mt, lds2, chunks_max);
     pl.ws_total = kTOffset + kTBytes;
   } else {
     pl.ws_total = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
@@ -1072,38 +1108,45 @@ void dispatch_latent(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
   }
 }
 
+template <typename YT, int MT, int S, int TILES>
+void launch_expand_mfma(const MfmaParams& p, int grid, size_t lds, hipStream_t s) {
+  using E = ExpandShape<TILES>;
+  hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S, TILES>), dim3(grid), dim3(E::THREADS), lds, s, p);
+}
+
 template <typename YT, int MT, int S>
-void launch_expand_mfma_s(const MfmaParams& p, int grid, size_t lds, hipStream_t s) {
-  using E = ExpandShape<MT>;
-  hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S>), dim3(grid), dim3(E::THREADS), lds, s, p);
+void dispatch_expand_tiles(const MfmaParams& p, int tiles, int grid, size_t lds, hipStream_t s) {
+  if constexpr (MT >= 4) {
+    if (tiles == 8) return launch_expand_mfma<YT, MT, S, 8>(p, grid, lds, s);
+  }
+  if (tiles == 4) return launch_expand_mfma<YT, MT, S, 4>(p, grid, lds, s);
+  launch_expand_mfma<YT, MT, S, 2>(p, grid, lds, s);
 }
 
 template <typename YT, int MT>
-void dispatch_expand_s(const MfmaParams& p, int wsteps, int grid, size_t lds, hipStream_t s) {
-  switch (wsteps) {
-    case 4: launch_expand_mfma_s<YT, MT, 4>(p, grid, lds, s); break;
-    case 8: launch_expand_mfma_s<YT, MT, 8>(p, grid, lds, s); break;
-    case 16: launch_expand_mfma_s<YT, MT, 16>(p, grid, lds, s); break;
-    default: launch_expand_mfma_s<YT, MT, kMaxWaveSteps>(p, grid, lds, s); break;
+void dispatch_expand_s(const MfmaParams& p, const Plan& pl, int grid, hipStream_t s) {
+  switch (pl.wsteps) {
+    case 4: dispatch_expand_tiles<YT, MT, 4>(p, pl.tiles, grid, pl.lds2, s); break;
+    case 8: dispatch_expand_tiles<YT, MT, 8>(p, pl.tiles, grid, pl.lds2, s); break;
+    case 16: dispatch_expand_tiles<YT, MT, 16>(p, pl.tiles, grid, pl.lds2, s); break;
+    default: dispatch_expand_tiles<YT, MT, kMaxWaveSteps>(p, pl.tiles, grid, pl.lds2, s); break;
   }
 }
 
 template <typename YT>
 void dispatch_expand(const MfmaParams& p, const Plan& pl, int grid, hipStream_t s) {
   switch (pl.mt) {
-    case 1: dispatch_expand_s<YT, 1>(p, pl.wsteps, grid, pl.lds2, s); break;
-    case 2: dispatch_expand_s<YT, 2>(p, pl.wsteps, grid, pl.lds2, s); break;
-    case 4: dispatch_expand_s<YT, 4>(p, pl.wsteps, grid, pl.lds2, s); break;
-    case 8: dispatch_expand_s<YT, 8>(p, pl.wsteps, grid, pl.lds2, s); break;
-    default: dispatch_expand_s<YT, 16>(p, pl.wsteps, grid, pl.lds2, s); break;
+    case 1: dispatch_expand_s<YT, 1>(p, pl, grid, s); break;
+    case 2: dispatch_expand_s<YT, 2>(p, pl, grid, s); break;
+    case 4: dispatch_expand_s<YT, 4>(p, pl, grid, s); break;
+    case 8: dispatch_expand_s<YT, 8>(p, pl, grid, s); break;
+    default: dispatch_expand_s<YT, 16>(p, pl, grid, s); break;
   }
 }
 
 int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
                  int y_dtype, void* workspace, hipStream_t s) {
-  using E1 = ExpandShape<1>;
-  using E4 = ExpandShape<4>;
-  const int rows = pl.mt >= 4 ? E4::ROWS : E1::ROWS;
+  const int rows = 16 * pl.tiles;
   MfmaParams p;
   memset(&p, 0, sizeof(p));
   p.nproj = np;
