@@ -238,7 +238,7 @@ def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5):
             "bytes_per_pass": b, "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32):
+def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, target=True):
     """Config 2 draft tokens and config 3 verification on whole Llama-2-7B-shaped
     models (random packed factors, |N|+0.05 scales; embedding and a bf16
     lm_head N(0,1)): attention, norms and lm_head in PyTorch, linears on the
@@ -282,6 +282,8 @@ def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32):
                     f"generate_draft_tokens_k{draft_len}_ms": round(a.elapsed_time(b), 3)}
     del draft, st
     torch.cuda.empty_cache()
+    if not target:
+        return out
     # --- config 3: 1.0-BPW target (draft + residual branch per projection), KV length 1024
     st = synthetic_runtime_state(cfg, C["draft_rank"], C["residual_rank"], seed=2, device=dev)
     target = GPUTargetModel(draft_state=st, config=cfg, device=dev, max_seq_len=kv_target + 64,
@@ -373,7 +375,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
-    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "verify", "copy"], default=None,
+    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -404,8 +406,8 @@ def main():
         print(json.dumps({"only": "copy", "bytes_read_per_copy": 4 * n, "bytes_written_per_copy": 4 * n,
                           "copies": max(args.steps, 1)}))
         return
-    if args.only == "decode":
-        print(json.dumps(decode_bench(dev)))
+    if args.only in ("decode", "draft"):
+        print(json.dumps(decode_bench(dev, target=args.only == "decode")))
         return
     if args.only == "verify":
         print(json.dumps(verify_linears_bench(gen, dev, stream, args.layers, steps=args.steps, warmup=args.warmup)))

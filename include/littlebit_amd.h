@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 1
+#define LBK_ABI_VERSION 2
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -60,14 +60,32 @@ typedef struct lbk_branch {
 } lbk_branch;
 
 /* One projection of a group call: its branches (1 or 2), out_features N,
- * optional fp32 bias [N] and output y [M, N] (of the call's y_dtype). */
+ * optional fp32 bias [N], output y [M, N] (of the call's y_dtype) and an
+ * optional fp32 residual [M, N] added to y (it may be y itself: the update
+ * x += projection(...) of a decoder layer). */
 typedef struct lbk_projection {
   const lbk_branch* branches;
   int n_branches;
   int64_t out_features;
   const float* bias;
   void* y;
+  const float* residual;
 } lbk_projection;
+
+/* What the projections of a call read (the reference's CPU decode step
+ * applies these inline, patches/littlebit_cpu_optimized.cpp:1370-1438):
+ *   LBK_INPUT_PLAIN     x
+ *   LBK_INPUT_RMSNORM   x[m, k] / sqrt(mean_k x[m, k]^2 + rms_eps) * rms_weight[k]
+ *   LBK_INPUT_SILU_MUL  x[m, k] / (1 + exp(-x[m, k])) * x1[m, k]  (x = gate, x1 = up) */
+#define LBK_INPUT_PLAIN 0
+#define LBK_INPUT_RMSNORM 1
+#define LBK_INPUT_SILU_MUL 2
+typedef struct lbk_input {
+  int kind;
+  const float* rms_weight; /* [K] fp32 (RMSNORM) */
+  float rms_eps;
+  const void* x1;          /* [M, K] of x_dtype (SILU_MUL) */
+} lbk_input;
 
 #define LBK_MAX_GROUP 4
 
@@ -110,6 +128,12 @@ int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M,
                       int64_t K, const void* x, int x_dtype, int y_dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* lbk_group_forward with a fused input transform (input NULL = plain). */
+int lbk_group_forward_ex(const lbk_projection* projs, int n_proj, int64_t M,
+                         int64_t K, const void* x, int x_dtype,
+                         const lbk_input* input, int y_dtype, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* One-branch form with the argument list of the reference operator
  * littlebit_cpu_ops::littlebit_linear (patches/littlebit_cpu_optimized.cpp:
  * 598-701, schema at :2324-2329): input [M, v_cols] fp32, v2 [1, v_cols],
@@ -122,6 +146,25 @@ int lbk_littlebit_linear(const float* input, int64_t M, const float* v2,
                          int64_t u_cols, const float* u1, int64_t out_features,
                          float* output, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* Decode attention of one query token (the draft step's attention), fp32,
+ * kv_heads dividing heads, no rotary embedding, head_dim 64 or 128:
+ *   out[h] = sum_t softmax_t(scale * q[h] . K[h/r][t]) V[h/r][t], t = 0..pos
+ * where K/V[.][pos] are the new k, v [kv_heads * head_dim], which are also
+ * stored into k_cache / v_cache [kv_heads][max_seq][head_dim].  pos is read
+ * from pos_device when it is not NULL (so a captured graph follows a
+ * position the device advances), else taken from pos.  partial: scratch of
+ * lbk_attention_partial_bytes() (needed when max_seq > 32).  A position
+ * outside [0, max_seq) stores nothing and yields zeros.
+ * Replaces fused_attention_inline (patches/littlebit_cpu_optimized.cpp:
+ * 1441-1510) and the per-token attention of cpu_draft_model.py:371-383. */
+size_t lbk_attention_partial_bytes(int heads, int max_seq, int head_dim);
+int lbk_attention_decode(const float* q, const float* k, const float* v,
+                         float* k_cache, float* v_cache, int heads,
+                         int kv_heads, int head_dim, int max_seq,
+                         const int64_t* pos_device, int64_t pos, float scale,
+                         float* partial, size_t partial_bytes, float* out,
+                         void* stream);
 
 /* Expand packed signs to int8 {-1,+1}: out [rows, cols].
  * Replaces binary_unpacker (quantization/utils/binary_packer.py:54-97). */

@@ -56,9 +56,24 @@ class LbkProjection(ctypes.Structure):
         ("out_features", ctypes.c_int64),
         ("bias", ctypes.c_void_p),
         ("y", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
     ]
 
 
+class LbkInput(ctypes.Structure):
+    """Mirror of ``lbk_input``."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int),
+        ("rms_weight", ctypes.c_void_p),
+        ("rms_eps", ctypes.c_float),
+        ("x1", ctypes.c_void_p),
+    ]
+
+
+LBK_INPUT_PLAIN = 0
+LBK_INPUT_RMSNORM = 1
+LBK_INPUT_SILU_MUL = 2
 LBK_MAX_GROUP = 4
 
 # name -> (restype, argtypes); must list every function of include/littlebit_amd.h
@@ -79,9 +94,20 @@ SIGNATURES = {
         [ctypes.POINTER(LbkProjection), ctypes.c_int, _I64, _I64, _VP, ctypes.c_int, ctypes.c_int, _VP,
          ctypes.c_size_t, _VP],
     ),
+    "lbk_group_forward_ex": (
+        ctypes.c_int,
+        [ctypes.POINTER(LbkProjection), ctypes.c_int, _I64, _I64, _VP, ctypes.c_int, ctypes.POINTER(LbkInput),
+         ctypes.c_int, _VP, ctypes.c_size_t, _VP],
+    ),
     "lbk_littlebit_linear": (
         ctypes.c_int,
         [_VP, _I64, _VP, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, ctypes.c_size_t, _VP],
+    ),
+    "lbk_attention_partial_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "lbk_attention_decode": (
+        ctypes.c_int,
+        [_VP, _VP, _VP, _VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP, _I64,
+         ctypes.c_float, _VP, ctypes.c_size_t, _VP, _VP],
     ),
     "lbk_unpack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
     "lbk_pack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),

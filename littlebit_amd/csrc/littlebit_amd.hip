@@ -135,6 +135,7 @@ struct ExpProj {
   const uint32_t* U[2];  // [N, RW] sign words per branch
   const float* h[2];     // [N]
   const float* bias;     // [N] or null
+  const float* res;      // [M, N] fp32 added to y, or null (may alias y)
   void* y;               // [M, N]
   int RW[2];    // words per U row
   int RWp[2];   // RW rounded up to a multiple of 4
@@ -152,8 +153,12 @@ struct MfmaParams {
   int M, K, KW;
   int tsize;    // M * sum(RP) floats
   int nkc;      // k-chunks
-  int xvec;     // x and every g allow 16-byte loads (aligned, K % 8 == 0)
+  int xvec;     // x (x1, rms weight) and every g allow 16-byte loads (aligned, K % 8 == 0)
+  int xmode;    // LBK_INPUT_*: x as is, RMSNorm(x) * w, or SiLU(x) * x1
   const void* x;
+  const void* x1;       // second input of LBK_INPUT_SILU_MUL
+  const float* nw;      // RMSNorm weight [K]
+  float eps;            // RMSNorm epsilon
   float* t2;       // two halves of kTHalf floats; per segment [M][RP] latent, l-scaled
   uint32_t* sync;  // [0] P: half the next latent kernel accumulates into
                    // [1] Q: half the last latent kernel accumulated into
@@ -225,6 +230,85 @@ struct Compact {
     return ml < MR ? (col < 8 ? ml : MR + ml) : 2 * MR;
   }
 };
+
+// The effective input of a call, element (m, k) times g[k]:
+//   LBK_INPUT_PLAIN     x[m, k]
+//   LBK_INPUT_RMSNORM   x[m, k] * rs[m] * w[k],  rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps)
+//   LBK_INPUT_SILU_MUL  x[m, k] / (1 + exp(-x[m, k])) * x1[m, k]
+// (the RMSNorm, SiLU * up and their order are those of the reference's CPU
+// decode step, patches/littlebit_cpu_optimized.cpp:1370-1438).
+__device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
+
+// rs[m] for m < M: every thread sums x[m, k]^2 over k = tid, tid + BLOCK, ..;
+// waves reduce by shuffles, then one LDS pass.  Ends with a barrier.
+template <typename XT, int MT, int BLOCK>
+__device__ __forceinline__ void rms_scales(const XT* __restrict__ x, int M, int K, float eps, float* rs,
+                                           float* scratch /* [BLOCK / 64][MT] */, int tid) {
+  float part[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) part[m] = 0.f;
+  for (int k = tid; k < K; k += BLOCK) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = m < M ? to_f32(x[size_t(m) * K + k]) : 0.f;
+      part[m] += v * v;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) part[m] += __shfl_xor(part[m], o);
+  }
+  if ((tid & 63) == 0) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) scratch[(tid >> 6) * MT + m] = part[m];
+  }
+  __syncthreads();
+  if (tid < MT) {
+    float ssum = 0.f;
+    for (int w = 0; w < BLOCK / 64; ++w) ssum += scratch[w * MT + tid];
+    rs[tid] = 1.f / sqrtf(ssum / float(K) + eps);
+  }
+  __syncthreads();
+}
+
+// 8 effective inputs (m, kb .. kb+7) times g, zeros past K.
+template <typename XT>
+__device__ __forceinline__ void load_input8(const MfmaParams& p, const float* __restrict__ g, int m, int kb,
+                                            float rsm, float (&a)[8]) {
+  const XT* __restrict__ x = static_cast<const XT*>(p.x) + size_t(m) * p.K;
+  const int K = p.K;
+  if (p.xvec && kb + 8 <= K) {
+    float gv[8];
+    load8(x + kb, a);
+    load8(g + kb, gv);
+    if (p.xmode == LBK_INPUT_RMSNORM) {
+      float wv[8];
+      load8(p.nw + kb, wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) gv[i] *= wv[i] * rsm;
+    } else if (p.xmode == LBK_INPUT_SILU_MUL) {
+      float uv[8];
+      load8(static_cast<const XT*>(p.x1) + size_t(m) * K + kb, uv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = silu_f(a[i]) * uv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] *= gv[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = 0.f;
+      if (kb + i < K) {
+        v = to_f32(x[kb + i]) * g[kb + i];
+        if (p.xmode == LBK_INPUT_RMSNORM) v *= p.nw[kb + i] * rsm;
+        else if (p.xmode == LBK_INPUT_SILU_MUL)
+          v = silu_f(to_f32(x[kb + i])) * to_f32(static_cast<const XT*>(p.x1)[size_t(m) * K + kb + i]) * g[kb + i];
+      }
+      a[i] = v;
+    }
+  }
+}
 
 // Blocks are dispatched to the 8 XCDs of MI355X round-robin (block b runs on
 // XCD b % 8, confirmed on the device).  This maps block b to a logical index
@@ -325,25 +409,15 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   const uint32_t s0 = p.sync[2];
   const uint32_t s1 = p.sync[3];
 
-  // ---- A operand: hi/lo bf16 of g[k] * x[m, k] for this k-chunk ----
-  {
-    const XT* __restrict__ x = static_cast<const XT*>(p.x);
-    const int K = p.K;
-    const bool xvec = p.xvec != 0;
-    build_compact<MT, kBlock>(lds_a, NCH, p.M, tid, [&](int c, int m, float (&a)[8]) {
-      const int kb = k0 + 8 * c;
-      if (xvec && kb + 8 <= K) {
-        load8(x + size_t(m) * K + kb, a);
-        float gv[8];
-        load8(g + kb, gv);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] *= gv[i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = (kb + i < K) ? g[kb + i] * to_f32(x[size_t(m) * K + kb + i]) : 0.f;
-      }
-    });
+  // ---- A operand: hi/lo bf16 of g[k] * input[m, k] for this k-chunk ----
+  __shared__ float rs[MT];
+  if (p.xmode == LBK_INPUT_RMSNORM) {
+    __shared__ float rscratch[kBlock / 64 * MT];
+    rms_scales<XT, MT, kBlock>(static_cast<const XT*>(p.x), p.M, p.K, p.eps, rs, rscratch, tid);
   }
+  build_compact<MT, kBlock>(lds_a, NCH, p.M, tid, [&](int c, int m, float (&a)[8]) {
+    load_input8<XT>(p, g, m, k0 + 8 * c, p.xmode == LBK_INPUT_RMSNORM ? rs[m] : 1.f, a);
+  });
   __syncthreads();
 
   uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
@@ -557,13 +631,17 @@ __global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kerne
   if (half == 0 && lane < 32 && nvalid) {
     const float bn = P.bias ? P.bias[n] : 0.f;
     YT* y = static_cast<YT*>(P.y);
+    const float* res = P.res;
     const int N = P.N;
 #pragma unroll
     for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = mb * 8 + grp * 4 + i;
-        if (m < p.M) store_out(y, size_t(m) * N + n, out[mb][i] + red[tile][mb * 4 + i][lane] + bn);
+        if (m < p.M) {
+          const size_t o = size_t(m) * N + n;
+          store_out(y, o, out[mb][i] + red[tile][mb * 4 + i][lane] + bn + (res ? res[o] : 0.f));
+        }
       }
   }
 
@@ -615,6 +693,7 @@ struct GemmProj {     // stage-2 operands of one projection
   const uint32_t* U[2];
   const float* h[2];
   const float* bias;
+  const float* res;   // [M, N] fp32 added to y, or null (may alias y)
   void* y;
   int RW[2];          // words per U row
   int RP[2];
@@ -630,8 +709,12 @@ struct GemmParams {
   int nseg, nproj;
   int M, K, KW;
   int Kp;             // K rounded up to kGK
-  int xvec;           // x rows and every g allow 16-byte loads
+  int xvec;           // x rows (x1, rms weight) and every g allow 16-byte loads
+  int xmode;          // LBK_INPUT_* (see load_input8)
   const void* x;
+  const void* x1;
+  const float* nw;
+  float eps;
   uint16_t* a;        // A planes (hi, then lo with SPLIT)
   uint16_t* t;        // T planes
   int64_t a_plane;    // elements per A plane
@@ -645,24 +728,54 @@ __device__ __forceinline__ void split1(float v, uint16_t& hi, uint16_t& lo) {
 }
 
 // Prologue.  grid = (M, segments), 256 threads; thread handles 8-k chunks.
+// The input mode (RMSNorm, SiLU * up) is applied here, as in load_input8.
 template <typename XT, bool SPLIT>
 __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
   const int m = int(blockIdx.x);
   const GemmSeg& S = p.seg[__builtin_amdgcn_readfirstlane(int(blockIdx.y))];
   const XT* __restrict__ xr = static_cast<const XT*>(p.x) + int64_t(m) * p.K;
+  const XT* __restrict__ ur = p.x1 ? static_cast<const XT*>(p.x1) + int64_t(m) * p.K : xr;
   const float* __restrict__ g = S.g;
+  const int tid = int(threadIdx.x);
+  float rsm = 1.f;
+  if (p.xmode == LBK_INPUT_RMSNORM) {
+    __shared__ float rs[1];
+    __shared__ float rscratch[kGThreads / 64];
+    rms_scales<XT, 1, kGThreads>(xr, 1, p.K, p.eps, rs, rscratch, tid);
+    rsm = rs[0];
+  }
   uint16_t* __restrict__ hi = p.a + S.abase + int64_t(m) * p.Kp;
-  for (int k = 8 * int(threadIdx.x); k < p.Kp; k += 8 * kGThreads) {
+  for (int k = 8 * tid; k < p.Kp; k += 8 * kGThreads) {
     float v[8];
     if (p.xvec && k + 8 <= p.K) {
       float gv[8];
       load8(xr + k, v);
       load8(g + k, gv);
+      if (p.xmode == LBK_INPUT_RMSNORM) {
+        float wv[8];
+        load8(p.nw + k, wv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) gv[i] *= wv[i] * rsm;
+      } else if (p.xmode == LBK_INPUT_SILU_MUL) {
+        float uv[8];
+        load8(ur + k, uv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = silu_f(v[i]) * uv[i];
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] *= gv[i];
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (k + i < p.K) ? g[k + i] * to_f32(xr[k + i]) : 0.f;
+      for (int i = 0; i < 8; ++i) {
+        float e = 0.f;
+        if (k + i < p.K) {
+          const float xv = to_f32(xr[k + i]);
+          e = xv * g[k + i];
+          if (p.xmode == LBK_INPUT_RMSNORM) e *= p.nw[k + i] * rsm;
+          else if (p.xmode == LBK_INPUT_SILU_MUL) e = silu_f(xv) * to_f32(ur[k + i]) * g[k + i];
+        }
+        v[i] = e;
+      }
     }
     if constexpr (SPLIT) {
       u32x4 h, l;
@@ -874,12 +987,16 @@ __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
     const float h0 = P.h[0][n];
     const float h1 = P.nb > 1 ? P.h[1][n] : 0.f;
     const float bn = P.bias ? P.bias[n] : 0.f;
+    const float* res = P.res;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
-        if (m < p.M) store_out(y, size_t(m) * P.N + n, h0 * acc0[i][j][q] + h1 * acc1[i][j][q] + bn);
+        if (m < p.M) {
+          const size_t o = size_t(m) * P.N + n;
+          store_out(y, o, h0 * acc0[i][j][q] + h1 * acc1[i][j][q] + bn + (res ? res[o] : 0.f));
+        }
       }
   }
 }
@@ -914,6 +1031,213 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention: one query token per sequence, fp32, grouped KV heads,
+// no rotary embedding (fused_attention_inline,
+// patches/littlebit_cpu_optimized.cpp:1441-1510):
+//   out[h] = sum_t softmax_t(scale * q[h] . K[h / rep][t]) V[h / rep][t],
+//   t = 0 .. pos, with K/V[.][pos] = the new k, v, which are also stored in
+//   the cache [kv_heads][max_seq][HD].
+// grid = (heads, chunks of kAttnChunk positions), 256 threads.  A block
+// scores its chunk with coalesced row reads (a group of lanes per K row,
+// shuffle reduction), takes the chunk's max and exp-sum, and accumulates
+// p . V with each wave on a quarter of the positions.  With one chunk it
+// writes out directly, otherwise (max, sum, o[HD]) per chunk, which
+// attn_combine_kernel merges.  pos is read on the device when pos_ptr is set (graph replay);
+// pos >= max_seq writes nothing but zeros to out.
+// ---------------------------------------------------------------------------
+constexpr int kAttnChunk = 32;
+constexpr int kAttnThreads = 256;
+
+struct AttnParams {
+  const float* q;        // [heads * HD]
+  const float* k;        // [kv_heads * HD]  new key
+  const float* v;        // [kv_heads * HD]  new value
+  float* kc;             // [kv_heads][max_seq][HD]
+  float* vc;
+  const int64_t* pos_ptr;
+  int64_t pos;
+  int heads, rep, max_seq, chunks;
+  float scale;
+  float* part;           // [heads][chunks][HD + 2]
+  float* out;            // [heads * HD]
+};
+
+__device__ __forceinline__ int64_t attn_pos(const AttnParams& p) { return p.pos_ptr ? *p.pos_ptr : p.pos; }
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p) {
+  // scores: LPR lanes read one K row (4 dims each) and reduce by shuffles, so
+  // a wave's load covers RPI whole rows; each wave takes PW positions.
+  // p . V: each wave takes the same PW positions, a lane DPL dimensions.
+  constexpr int LPR = HD / 4, RPI = 64 / LPR, NW = kAttnThreads / 64, PW = kAttnChunk / NW, DPL = HD / 64;
+  static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+  const int h = int(blockIdx.x), c = int(blockIdx.y), tid = int(threadIdx.x);
+  const int wave = tid >> 6, lane = tid & 63;
+  const int kv = h / p.rep;
+  const int64_t pos = attn_pos(p);
+  float* part = p.part + (size_t(h) * p.chunks + c) * (HD + 2);
+  if (pos < 0 || pos >= p.max_seq) {  // out of range: nothing is read or stored
+    if (c == 0 && tid < HD) p.out[size_t(h) * HD + tid] = 0.f;
+    return;
+  }
+  const int S = int(pos) + 1;
+  const int t0 = c * kAttnChunk, t1 = min(t0 + kAttnChunk, S);
+  if (t0 >= t1) {  // chunk past the current length: an empty partial
+    if (tid < HD) part[tid] = 0.f;
+    if (tid == 0) {
+      part[HD] = -INFINITY;
+      part[HD + 1] = 0.f;
+    }
+    return;
+  }
+  const float* kn = p.k + size_t(kv) * HD;
+  const float* vn = p.v + size_t(kv) * HD;
+  float* kc = p.kc + size_t(kv) * p.max_seq * HD;
+  float* vc = p.vc + size_t(kv) * p.max_seq * HD;
+  if (c == 0 && (h % p.rep) == 0 && tid < HD) {  // store the new key / value (read below from kn, vn)
+    kc[size_t(pos) * HD + tid] = kn[tid];
+    vc[size_t(pos) * HD + tid] = vn[tid];
+  }
+  __shared__ float qs[HD];
+  __shared__ float ps[kAttnChunk];
+  __shared__ float wred[NW];
+  __shared__ float ored[NW][HD];
+  const bool full = t1 - t0 == kAttnChunk && !(pos >= t0 && pos < t1);  // no tail, no new row
+  const int d0 = lane * DPL;
+  float vv[PW][DPL];  // a full chunk's V rows, loaded before anything waits
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < PW; ++it) {
+      const float* vr = vc + size_t(t0 + wave * PW + it) * HD + d0;
+      if constexpr (DPL == 2) {
+        const float2 w2 = *reinterpret_cast<const float2*>(vr);
+        vv[it][0] = w2.x;
+        vv[it][DPL - 1] = w2.y;
+      } else {
+        vv[it][0] = vr[0];
+      }
+    }
+  }
+  if (tid < HD) qs[tid] = p.q[size_t(h) * HD + tid] * p.scale;
+  __syncthreads();
+  const int sub = lane / LPR, dl = (lane % LPR) * 4;
+  const float4 q4 = *reinterpret_cast<const float4*>(qs + dl);
+  if (full) {  // every load first, then the arithmetic
+    float4 kk[PW / RPI];
+#pragma unroll
+    for (int it = 0; it < PW / RPI; ++it)
+      kk[it] = *reinterpret_cast<const float4*>(kc + size_t(t0 + wave * PW + it * RPI + sub) * HD + dl);
+#pragma unroll
+    for (int it = 0; it < PW / RPI; ++it) {
+      float d = q4.x * kk[it].x + q4.y * kk[it].y + q4.z * kk[it].z + q4.w * kk[it].w;
+#pragma unroll
+      for (int o = LPR / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
+      if ((lane % LPR) == 0) ps[wave * PW + it * RPI + sub] = d;
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < PW / RPI; ++it) {
+      const int i = wave * PW + it * RPI + sub;
+      const int t = t0 + i;
+      float d = 0.f;
+      if (t < t1) {
+        const float* kr = (t == pos) ? kn : kc + size_t(t) * HD;
+        const float4 kk = *reinterpret_cast<const float4*>(kr + dl);
+        d = q4.x * kk.x + q4.y * kk.y + q4.z * kk.z + q4.w * kk.w;
+      }
+#pragma unroll
+      for (int o = LPR / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
+      if ((lane % LPR) == 0) ps[i] = (t < t1) ? d : -INFINITY;
+    }
+  }
+  __syncthreads();
+  // chunk max and exp-sum (threads 0 .. kAttnChunk-1 hold one position each)
+  const float sc = tid < kAttnChunk ? ps[tid] : -INFINITY;
+  float mx = sc;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) wred[wave] = mx;
+  __syncthreads();
+  mx = wred[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, wred[w]);
+  const float e = (tid < kAttnChunk && t0 + tid < t1) ? __expf(sc - mx) : 0.f;
+  float sm = e;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sm += __shfl_xor(sm, o);
+  __syncthreads();  // every thread has read wred (max) and ps (scores)
+  if (tid < kAttnChunk) ps[tid] = e;
+  if (lane == 0) wred[wave] = sm;
+  __syncthreads();
+  sm = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) sm += wred[w];
+  // p . V over this wave's positions
+  float o[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) o[j] = 0.f;
+  if (full) {
+#pragma unroll
+    for (int it = 0; it < PW; ++it) {
+      const float pi = ps[wave * PW + it];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j] += pi * vv[it][j];
+    }
+  } else {
+    for (int it = 0; it < PW; ++it) {
+      const int i = wave * PW + it;
+      const int t = t0 + i;
+      if (t < t1) {
+        const float* vr = (t == pos) ? vn : vc + size_t(t) * HD;
+        const float pi = ps[i];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) o[j] += pi * vr[d0 + j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) ored[wave][d0 + j] = o[j];
+  __syncthreads();
+  if (tid < HD) {
+    float od = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) od += ored[w][tid];
+    if (p.chunks == 1) {
+      p.out[size_t(h) * HD + tid] = od / sm;
+    } else {
+      part[tid] = od;
+      if (tid == 0) {
+        part[HD] = mx;
+        part[HD + 1] = sm;
+      }
+    }
+  }
+}
+
+// out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c, in one pass
+// with a running maximum (each step rescales what it has).  grid = heads.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
+  const int h = int(blockIdx.x), d = int(threadIdx.x);
+  const int64_t pos = attn_pos(p);
+  if (pos < 0 || pos >= p.max_seq) return;  // out was zeroed by attn_decode_kernel
+  const float* part = p.part + size_t(h) * p.chunks * (HD + 2);
+  const int used = int(pos / kAttnChunk) + 1;  // chunks past pos hold empty partials
+  float M = -INFINITY, num = 0.f, den = 0.f;
+#pragma unroll 4
+  for (int c = 0; c < used; ++c) {
+    const float* pc = part + size_t(c) * (HD + 2);
+    const float mc = pc[HD], lc = pc[HD + 1], oc = pc[d];
+    const float Mn = fmaxf(M, mc);
+    const float a = __expf(M - Mn), b = __expf(mc - Mn);  // M = -inf at first: a = 0
+    num = num * a + oc * b;
+    den = den * a + lc * b;
+    M = Mn;
+  }
+  p.out[size_t(h) * HD + d] = num / den;
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -932,7 +1256,18 @@ struct ProjDesc {
   int64_t N;
   const float* bias;
   void* y;
+  const float* res;
 };
+
+// The call's effective input (LBK_INPUT_*).
+struct InputDesc {
+  int kind;
+  const float* nw;
+  float eps;
+  const void* x1;
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
 
 int validate_group(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   if (np < 1 || np > kMaxProj) return set_error(LBK_ERR_ARG, "n_proj must be in [1, %d], got %d", kMaxProj, np);
@@ -1145,7 +1480,7 @@ void dispatch_expand(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
 }
 
 int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
-                 int y_dtype, void* workspace, hipStream_t s) {
+                 const InputDesc& in, int y_dtype, void* workspace, hipStream_t s) {
   const int rows = 16 * pl.tiles;
   MfmaParams p;
   memset(&p, 0, sizeof(p));
@@ -1153,13 +1488,18 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
-  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  p.xmode = in.kind;
+  p.x1 = in.x1;
+  p.nw = in.nw;
+  p.eps = in.eps;
+  bool xvec = (K % 8) == 0 && aligned16(x) && (!in.x1 || aligned16(in.x1)) && (!in.nw || aligned16(in.nw));
   int rb = 0, tbase = 0, si = 0, tile = 0;
   for (int q = 0; q < np; ++q) {
     ExpProj& P = p.proj[q];
     P.nb = pd[q].nb;
     P.N = int(pd[q].N);
     P.bias = pd[q].bias;
+    P.res = pd[q].res;
     P.y = pd[q].y;
     P.tile0 = tile;
     tile += int(ceil_div(pd[q].N, rows));
@@ -1206,8 +1546,8 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   return check_launch("expand_mfma_kernel");
 }
 
-int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, int y_dtype,
-                 void* workspace, hipStream_t s) {
+int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, const InputDesc& in,
+                 int y_dtype, void* workspace, hipStream_t s) {
   const bool split = x_dtype == LBK_F32;
   GemmParams p;
   memset(&p, 0, sizeof(p));
@@ -1221,7 +1561,11 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
   char* ws = static_cast<char*>(workspace) + kGemmOffset;
   p.a = reinterpret_cast<uint16_t*>(ws);
   p.t = reinterpret_cast<uint16_t*>(ws + align256(size_t(p.a_plane) * (split ? 2 : 1) * sizeof(uint16_t)));
-  bool xvec = (K % 8) == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+  p.xmode = in.kind;
+  p.x1 = in.x1;
+  p.nw = in.nw;
+  p.eps = in.eps;
+  bool xvec = (K % 8) == 0 && aligned16(x) && (!in.x1 || aligned16(in.x1)) && (!in.nw || aligned16(in.nw));
   int si = 0, nt1 = 0, nt2 = 0;
   int64_t abase = 0, tbase = 0;
   for (int q = 0; q < np; ++q) {
@@ -1229,6 +1573,7 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
     P.nb = pd[q].nb;
     P.N = int(pd[q].N);
     P.bias = pd[q].bias;
+    P.res = pd[q].res;
     P.y = pd[q].y;
     P.nt0 = nt2;
     nt2 += int(ceil_div(pd[q].N, kGB));
@@ -1279,10 +1624,27 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
   return check_launch("gemm_expand_kernel");
 }
 
-int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype, int y_dtype,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype,
+                  const lbk_input* input, int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = validate_group(pd, np, M, K);
   if (rc != LBK_OK) return rc;
+  InputDesc in{LBK_INPUT_PLAIN, nullptr, 0.f, nullptr};
+  if (input) {
+    in = InputDesc{input->kind, input->rms_weight, input->rms_eps, input->x1};
+    if (in.kind == LBK_INPUT_RMSNORM) {
+      if (!in.nw) return set_error(LBK_ERR_ARG, "LBK_INPUT_RMSNORM needs rms_weight");
+      if (!(in.eps >= 0.f)) return set_error(LBK_ERR_ARG, "rms_eps must be >= 0");
+      in.x1 = nullptr;
+    } else if (in.kind == LBK_INPUT_SILU_MUL) {
+      if (!in.x1) return set_error(LBK_ERR_ARG, "LBK_INPUT_SILU_MUL needs x1");
+      in.nw = nullptr;
+    } else if (in.kind == LBK_INPUT_PLAIN) {
+      in.nw = nullptr;
+      in.x1 = nullptr;
+    } else {
+      return set_error(LBK_ERR_ARG, "input kind %d unknown", in.kind);
+    }
+  }
   if (x_dtype != LBK_F32 && x_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "x_dtype %d unsupported", x_dtype);
   if (y_dtype != LBK_F32 && y_dtype != LBK_BF16) return set_error(LBK_ERR_DTYPE, "y_dtype %d unsupported", y_dtype);
   if (M == 0) return LBK_OK;
@@ -1293,8 +1655,8 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
   if (!workspace || workspace_bytes < pl.ws_total)
     return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.mfma) return forward_mfma(pd, np, pl, M, K, x, x_dtype, y_dtype, workspace, s);
-  return forward_gemm(pd, np, M, K, x, x_dtype, y_dtype, workspace, s);
+  if (pl.mfma) return forward_mfma(pd, np, pl, M, K, x, x_dtype, in, y_dtype, workspace, s);
+  return forward_gemm(pd, np, M, K, x, x_dtype, in, y_dtype, workspace, s);
 }
 
 }  // namespace
@@ -1312,24 +1674,31 @@ size_t lbk_group_workspace_bytes(const lbk_projection* projs, int n_proj, int64_
     return 0;
   }
   for (int q = 0; q < n_proj; ++q)
-    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y};
+    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y,
+                     projs[q].residual};
   if (validate_group(pd, n_proj, M, K) != LBK_OK) return 0;
   return make_plan(pd, n_proj, M, K).ws_total;
 }
 
-int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x, int x_dtype,
-                      int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+int lbk_group_forward_ex(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x, int x_dtype,
+                         const lbk_input* input, int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error[0] = '\0';
   if (!projs || n_proj < 1 || n_proj > kMaxProj)
     return set_error(LBK_ERR_ARG, "n_proj must be in [1, %d] with a non-NULL array, got %d", kMaxProj, n_proj);
   ProjDesc pd[kMaxProj];
   for (int q = 0; q < n_proj; ++q)
-    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y};
-  return forward_group(pd, n_proj, M, K, x, x_dtype, y_dtype, workspace, workspace_bytes, stream);
+    pd[q] = ProjDesc{projs[q].branches, projs[q].n_branches, projs[q].out_features, projs[q].bias, projs[q].y,
+                     projs[q].residual};
+  return forward_group(pd, n_proj, M, K, x, x_dtype, input, y_dtype, workspace, workspace_bytes, stream);
+}
+
+int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x, int x_dtype,
+                      int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return lbk_group_forward_ex(projs, n_proj, M, K, x, x_dtype, nullptr, y_dtype, workspace, workspace_bytes, stream);
 }
 
 size_t lbk_linear_workspace_bytes(const lbk_branch* branches, int n_branches, int64_t M, int64_t K, int64_t N) {
-  const ProjDesc pd{branches, n_branches, N, nullptr, nullptr};
+  const ProjDesc pd{branches, n_branches, N, nullptr, nullptr, nullptr};
   if (validate_group(&pd, 1, M, K) != LBK_OK) return 0;
   return make_plan(&pd, 1, M, K).ws_total;
 }
@@ -1338,8 +1707,8 @@ int lbk_linear_forward(const lbk_branch* branches, int n_branches, int64_t M, in
                        const void* x, int x_dtype, const float* bias, void* y, int y_dtype, void* workspace,
                        size_t workspace_bytes, void* stream) {
   g_last_error[0] = '\0';
-  const ProjDesc pd{branches, n_branches, N, bias, y};
-  return forward_group(&pd, 1, M, K, x, x_dtype, y_dtype, workspace, workspace_bytes, stream);
+  const ProjDesc pd{branches, n_branches, N, bias, y, nullptr};
+  return forward_group(&pd, 1, M, K, x, x_dtype, nullptr, y_dtype, workspace, workspace_bytes, stream);
 }
 
 int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const int32_t* v_sign, int64_t v_cols,
@@ -1380,6 +1749,53 @@ int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols, int32_t* out
   hipLaunchKernelGGL(pack_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), signs,
                      rows, cols, wpr, reinterpret_cast<uint32_t*>(out));
   return check_launch("pack_kernel");
+}
+
+size_t lbk_attention_partial_bytes(int heads, int max_seq, int head_dim) {
+  if (heads < 1 || max_seq < 1 || head_dim < 1) return 0;
+  const int64_t chunks = ceil_div(max_seq, kAttnChunk);
+  return size_t(heads) * size_t(chunks) * size_t(head_dim + 2) * sizeof(float);
+}
+
+int lbk_attention_decode(const float* q, const float* k, const float* v, float* k_cache, float* v_cache, int heads,
+                         int kv_heads, int head_dim, int max_seq, const int64_t* pos_device, int64_t pos,
+                         float scale, float* partial, size_t partial_bytes, float* out, void* stream) {
+  g_last_error[0] = '\0';
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0)
+    return set_error(LBK_ERR_ARG, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv_heads);
+  if (head_dim != 64 && head_dim != 128) return set_error(LBK_ERR_ARG, "head_dim must be 64 or 128, got %d", head_dim);
+  if (max_seq < 1 || max_seq > (1 << 24)) return set_error(LBK_ERR_ARG, "max_seq out of range: %d", max_seq);
+  if (!pos_device && (pos < 0 || pos >= max_seq))
+    return set_error(LBK_ERR_ARG, "pos %lld outside [0, %d)", (long long)pos, max_seq);
+  if (!q || !k || !v || !k_cache || !v_cache || !out) return set_error(LBK_ERR_ARG, "NULL pointer");
+  const int chunks = int(ceil_div(max_seq, kAttnChunk));
+  const size_t need = lbk_attention_partial_bytes(heads, max_seq, head_dim);
+  if (chunks > 1 && (!partial || partial_bytes < need))
+    return set_error(LBK_ERR_WORKSPACE, "partial buffer of %zu bytes needed, %zu given", need, partial_bytes);
+  AttnParams p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.pos_ptr = pos_device;
+  p.pos = pos;
+  p.heads = heads;
+  p.rep = heads / kv_heads;
+  p.max_seq = max_seq;
+  p.chunks = chunks;
+  p.scale = scale;
+  p.part = partial;
+  p.out = out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid{unsigned(heads), unsigned(chunks), 1u};
+  if (head_dim == 128) hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kAttnThreads), 0, s, p);
+  else hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kAttnThreads), 0, s, p);
+  int rc = check_launch("attn_decode_kernel");
+  if (rc != LBK_OK || chunks == 1) return rc;
+  if (head_dim == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(heads), dim3(128), 0, s, p);
+  else hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(heads), dim3(64), 0, s, p);
+  return check_launch("attn_combine_kernel");
 }
 
 }  // extern "C"

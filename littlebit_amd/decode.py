@@ -102,12 +102,15 @@ class LittleBitDecoder:
     ``state`` is a runtime-layout state dict (:func:`~littlebit_amd.runtime.
     convert_state_dict` keys).  ``residual`` selects the projections'
     in-module residual branches (``_r`` keys): None uses them where present,
-    False ignores them.
+    False ignores them.  ``fuse`` (default) runs the RMSNorms, SiLU * up and
+    the residual adds inside the LittleBitLinear calls, as the reference's
+    C++ step does inline; ``fuse=False`` runs them as separate PyTorch ops.
     """
 
     def __init__(self, state: Dict[str, torch.Tensor], config: DecoderConfig, device="cuda",
-                 max_seq_len: int = 4096, residual: Optional[bool] = None):
+                 max_seq_len: int = 4096, residual: Optional[bool] = None, fuse: bool = True):
         dev = torch.device(device)
+        self.fuse = bool(fuse)
         if dev.type != "cuda":
             raise RuntimeError("LittleBitDecoder runs on a GPU (the HIP kernels have no CPU path)")
         self.config = config
@@ -140,6 +143,12 @@ class LittleBitDecoder:
         self.k_cache = torch.zeros(shape, dtype=torch.float32, device=dev)
         self.v_cache = torch.zeros(shape, dtype=torch.float32, device=dev)
         self.cache_pos = 0
+        # one-token steps use the HIP decode attention (head_dim 64 or 128)
+        self._hip_attn = self.fuse and c.head_dim in (64, 128)
+        if self._hip_attn:
+            from . import _lib
+            nbytes = _lib.load().lbk_attention_partial_bytes(c.num_attention_heads, self.max_seq_len, c.head_dim)
+            self._attn_part = torch.empty(max(int(nbytes) // 4, 1), dtype=torch.float32, device=dev)
 
     def reset(self):
         """Forget the cached positions (the reference's _LBModelUnit.reset)."""
@@ -159,6 +168,8 @@ class LittleBitDecoder:
         N = q.shape[0]
         kvh, hd, rep = c.num_key_value_heads, c.head_dim, c.kv_repeat
         kc, vc = self.k_cache[li], self.v_cache[li]
+        if N == 1 and tree_mask is None and self._hip_attn:
+            return self._attention_hip(q, k, v, kc, vc, start, pos_t)
         k3 = k.view(N, kvh, hd).transpose(0, 1)
         v3 = v.view(N, kvh, hd).transpose(0, 1)
         if pos_t is None:
@@ -191,6 +202,19 @@ class LittleBitDecoder:
         out = torch.matmul(probs, vals)  # [kvh, rep*N, hd]
         return out.view(kvh, rep, N, hd).permute(2, 0, 1, 3).reshape(N, kvh * rep * hd)
 
+    def _attention_hip(self, q, k, v, kc, vc, start: int, pos_t: Optional[torch.Tensor]):
+        from . import _lib
+        c = self.config
+        out = torch.empty((1, c.num_attention_heads * c.head_dim), dtype=torch.float32, device=q.device)
+        q, k, v = (t.to(torch.float32).contiguous() for t in (q, k, v))
+        rc = _lib.load().lbk_attention_decode(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), c.num_attention_heads,
+            c.num_key_value_heads, c.head_dim, self.max_seq_len, None if pos_t is None else pos_t.data_ptr(),
+            int(start), float(c.attn_scale), self._attn_part.data_ptr(), self._attn_part.numel() * 4, out.data_ptr(),
+            torch.cuda.current_stream(q.device).cuda_stream)
+        _lib.check(rc, "lbk_attention_decode")
+        return out
+
     def forward_hidden(self, x: torch.Tensor, start: int, length: Optional[int] = None,
                        pos_t: Optional[torch.Tensor] = None,
                        tree_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -198,14 +222,25 @@ class LittleBitDecoder:
         eps = self.config.rms_norm_eps
         if length is None and pos_t is None:
             length = start + x.shape[0]
+        if not self.fuse:
+            for li, L in enumerate(self.layers):
+                h = rms_norm(x, L["ln1"], eps)
+                q, k, v = L["qkv"].forward(h)
+                a = self._attention(li, q, k, v, start, length, pos_t, tree_mask)
+                x = x + L["o"].forward(a)
+                h = rms_norm(x, L["ln2"], eps)
+                g, u = L["gate_up"].forward(h)
+                x = x + L["down"].forward(F.silu(g) * u)
+            return rms_norm(x, self.final_norm, eps)
+        # the norms, SiLU * up and the residual adds run inside the projection
+        # calls; x (a private copy) is updated in place by o and down
+        x = x.to(torch.float32).clone()
         for li, L in enumerate(self.layers):
-            h = rms_norm(x, L["ln1"], eps)
-            q, k, v = L["qkv"].forward(h)
+            q, k, v = L["qkv"].forward(x, rms_weight=L["ln1"], rms_eps=eps)
             a = self._attention(li, q, k, v, start, length, pos_t, tree_mask)
-            x = x + L["o"].forward(a)
-            h = rms_norm(x, L["ln2"], eps)
-            g, u = L["gate_up"].forward(h)
-            x = x + L["down"].forward(F.silu(g) * u)
+            L["o"].forward(a, out=x, residual=x)
+            g, u = L["gate_up"].forward(x, rms_weight=L["ln2"], rms_eps=eps)
+            L["down"].forward(g, out=x, residual=x, x_up=u)
         return rms_norm(x, self.final_norm, eps)
 
     def forward_batch(self, token_ids: Sequence[int], embed_tokens: torch.Tensor,

@@ -144,6 +144,7 @@ class LittleBitProjection:
             arr[i].u1 = b.u1.data_ptr()
             arr[i].rank = b.rank
         self._arr = arr
+        self._group = None
 
     @property
     def ranks(self) -> Tuple[int, ...]:
@@ -158,8 +159,16 @@ class LittleBitProjection:
         return int(n)
 
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
-                out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-        """y[..., N] = sum of branches (+ bias) for x[..., K] (fp32 or bf16)."""
+                out_dtype: Optional[torch.dtype] = None, *, rms_weight: Optional[torch.Tensor] = None,
+                rms_eps: float = 1e-6, x_up: Optional[torch.Tensor] = None,
+                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """y[..., N] = sum of branches (+ bias) for x[..., K] (fp32 or bf16);
+        the fusions of :meth:`LittleBitProjectionGroup.forward`."""
+        if rms_weight is not None or x_up is not None or residual is not None:
+            if self._group is None:
+                self._group = LittleBitProjectionGroup([self])
+            return self._group.forward(x, None if out is None else [out], out_dtype, rms_weight=rms_weight,
+                                       rms_eps=rms_eps, x_up=x_up, residuals=[residual])[0]
         _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
         _check(x.device == self.device, "input must be on the factors' device")
         _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
@@ -226,12 +235,24 @@ class LittleBitProjectionGroup:
         return int(n)
 
     def forward(self, x: torch.Tensor, outs: Optional[Sequence[torch.Tensor]] = None,
-                out_dtype: Optional[torch.dtype] = None) -> list:
+                out_dtype: Optional[torch.dtype] = None, *, rms_weight: Optional[torch.Tensor] = None,
+                rms_eps: float = 1e-6, x_up: Optional[torch.Tensor] = None,
+                residuals: Optional[Sequence[Optional[torch.Tensor]]] = None) -> list:
+        """Outputs of every projection for input x [..., K].
+
+        Fusions (the reference decode step's inline operations,
+        patch:1370-1438 and the residual adds at :1738-1750):
+          ``rms_weight``  the projections read RMSNorm(x) * rms_weight;
+          ``x_up``        they read SiLU(x) * x_up (x the gate output);
+          ``residuals``   per projection an fp32 [..., N] tensor added to its
+                          output; it may be the output tensor itself.
+        """
         _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
         _check(x.device == self.device, "input must be on the factors' device")
         _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
         _check(x.shape[-1] == self.in_features,
                f"input last dimension {x.shape[-1]} != in_features {self.in_features}")
+        _check(rms_weight is None or x_up is None, "rms_weight and x_up exclude each other")
         lead = tuple(x.shape[:-1])
         x2 = x.reshape(-1, self.in_features)
         if not x2.is_contiguous():
@@ -248,14 +269,32 @@ class LittleBitProjectionGroup:
                        "an output has the wrong shape, dtype or layout")
         if M == 0:
             return list(outs)
+        inp = None
+        keep = []
+        if rms_weight is not None:
+            _require_cuda(rms_weight, "rms_weight")
+            _check(rms_weight.dtype == torch.float32 and rms_weight.numel() == self.in_features,
+                   "rms_weight must be float32 with in_features elements")
+            inp = _lib.LbkInput(_lib.LBK_INPUT_RMSNORM, rms_weight.data_ptr(), float(rms_eps), None)
+        elif x_up is not None:
+            _require_cuda(x_up, "x_up")
+            _check(x_up.dtype == x.dtype and x_up.numel() == x.numel(), "x_up must match x in dtype and size")
+            inp = _lib.LbkInput(_lib.LBK_INPUT_SILU_MUL, None, 0.0, x_up.data_ptr())
         for i, o in enumerate(outs):
             self._arr[i].y = o.data_ptr()
+            r = None if residuals is None else residuals[i]
+            if r is not None:
+                _require_cuda(r, f"residuals[{i}]")
+                _check(r.dtype == torch.float32 and r.numel() == o.numel(), "a residual must be float32 like its output")
+                keep.append(r)
+            self._arr[i].residual = None if r is None else r.data_ptr()
         lib = _lib.load()
         stream = torch.cuda.current_stream(x.device).cuda_stream
         ws = workspace_for(x.device, stream, self.workspace_bytes(M))
-        rc = lib.lbk_group_forward(self._arr, len(self.projections), M, self.in_features, x2.data_ptr(),
-                                   _DTYPE_CODES[x.dtype], _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
-        _lib.check(rc, "lbk_group_forward")
+        rc = lib.lbk_group_forward_ex(self._arr, len(self.projections), M, self.in_features, x2.data_ptr(),
+                                      _DTYPE_CODES[x.dtype], ctypes.byref(inp) if inp is not None else None,
+                                      _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "lbk_group_forward_ex")
         return list(outs)
 
     __call__ = forward

@@ -16,6 +16,9 @@ bits), the reference's algorithm for the hot path:
   (main branch + optional residual branch + optional bias; the branches may
   have different ranks, which the reference module does not allow but its
   runtime layout does: convert_hf_to_runtime.py:66-84)
+* ``rms_norm``, ``silu_mul`` -- the inputs the reference's CPU decode step
+  feeds its projections: rms_norm_inline and silu_mul_inline,
+  patches/littlebit_cpu_optimized.cpp:1370-1405 and 1410-1438
 
 Every function here is pinned in ``tests/test_oracle.py`` by hand-derived
 golden words, textbook special cases, a brute-force dense evaluation built
@@ -28,6 +31,8 @@ import numpy as np
 __all__ = [
     "sign_pm1",
     "pack_signs",
+    "rms_norm",
+    "silu_mul",
     "unpack_signs",
     "words_per_row",
     "fuse_mid",
@@ -142,6 +147,18 @@ def littlebit_forward(x, branches, K: int, N: int, bias=None) -> np.ndarray:
     if bias is not None:
         y = y + np.asarray(bias, dtype=np.float64).reshape(1, N)
     return y.reshape(*lead, N)
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """x / sqrt(mean(x^2) + eps) * w over the last axis (patch:1370-1405)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps) * np.asarray(w, dtype=np.float64)
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """gate * sigmoid(gate) * up (patch:1410-1438)."""
+    g = np.asarray(gate, dtype=np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(up, dtype=np.float64)
 
 
 def rel_err(y, y_ref) -> float:

@@ -117,8 +117,27 @@ def _group(n, rank=8, N=64):
 
 def test_group_struct_layout():
     import littlebit_amd._lib as L
-    assert ctypes.sizeof(L.LbkProjection) == 40
+    assert ctypes.sizeof(L.LbkProjection) == 48
     assert L.LbkProjection.out_features.offset == 16 and L.LbkProjection.y.offset == 32
+    assert L.LbkProjection.residual.offset == 40
+    assert ctypes.sizeof(L.LbkInput) == 32
+    assert (L.LbkInput.rms_weight.offset, L.LbkInput.rms_eps.offset, L.LbkInput.x1.offset) == (8, 16, 24)
+
+
+def test_input_kind_validation():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    arr, keep = _group(2)
+    fx = lib.lbk_group_forward_ex
+    bad = L.LbkInput(7, None, 0.0, None)
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(bad), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "input kind" in L.last_error()
+    rms = L.LbkInput(L.LBK_INPUT_RMSNORM, None, 1e-6, None)
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(rms), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "rms_weight" in L.last_error()
+    silu = L.LbkInput(L.LBK_INPUT_SILU_MUL, None, 0.0, None)
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(silu), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "x1" in L.last_error()
 
 
 def test_group_validation_errors():

@@ -81,17 +81,64 @@ def ref_hidden(state, cfg, ids, residual):
     return norm(x, _np(state["model.norm.weight"]))
 
 
-@pytest.mark.parametrize("residual", [False, True])
-def test_decoder_matches_float64_reference(gpu, residual):
+@pytest.mark.parametrize("residual,fuse", [(False, True), (True, True), (True, False)])
+def test_decoder_matches_float64_reference(gpu, residual, fuse):
     from littlebit_amd.decode import LittleBitDecoder
     cfg = _cfg()
     st = _state(11)
-    dec = LittleBitDecoder(st, cfg, gpu, max_seq_len=64, residual=None if residual else False)
+    dec = LittleBitDecoder(st, cfg, gpu, max_seq_len=64, residual=None if residual else False, fuse=fuse)
     ids = [3, 17, 250, 9, 101, 42, 7]
     h = dec.forward_batch(ids, st["model.embed_tokens.weight"].to(gpu))
     err = O.rel_err(h.cpu().numpy(), ref_hidden(st, cfg, ids, residual))
     print(f"[decode] residual={residual} rel_err={err:.2e}", flush=True)
     assert err <= TOL
+
+
+@pytest.mark.parametrize("heads,kvh,hd,max_seq,pos", [(4, 2, 128, 64, 0), (4, 2, 128, 64, 37), (8, 8, 64, 400, 300),
+                                                      (32, 8, 128, 700, 513), (2, 1, 64, 256, 255)])
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_attention_decode_kernel(gpu, heads, kvh, hd, max_seq, pos, device_pos):
+    """lbk_attention_decode against torch: softmax(scale q.K) V over 0..pos,
+    the new k/v used at pos and stored into the cache."""
+    import littlebit_amd._lib as L
+    g = torch.Generator(device="cpu").manual_seed(pos + heads)
+    kc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    vc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    q = torch.randn((heads * hd,), generator=g).to(gpu)
+    k = torch.randn((kvh * hd,), generator=g).to(gpu)
+    v = torch.randn((kvh * hd,), generator=g).to(gpu)
+    scale = hd ** -0.5
+    K = kc.clone()
+    V = vc.clone()
+    K[:, pos] = k.view(kvh, hd)
+    V[:, pos] = v.view(kvh, hd)
+    rep = heads // kvh
+    qg = q.view(kvh, rep, hd).double().cpu()
+    s = torch.einsum("grd,gtd->grt", qg, K[:, :pos + 1].double().cpu()) * scale
+    ref = torch.einsum("grt,gtd->grd", torch.softmax(s, dim=-1), V[:, :pos + 1].double().cpu()).reshape(-1)
+    lib = L.load()
+    part = torch.empty(lib.lbk_attention_partial_bytes(heads, max_seq, hd) // 4 + 1, device=gpu)
+    out = torch.full((heads * hd,), float("nan"), device=gpu)
+    pos_t = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    rc = lib.lbk_attention_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads, kvh,
+                                  hd, max_seq, pos_t.data_ptr() if device_pos else None, 0 if device_pos else pos,
+                                  scale, part.data_ptr(), part.numel() * 4, out.data_ptr(), None)
+    L.check(rc, "lbk_attention_decode")
+    torch.cuda.synchronize()
+    assert O.rel_err(out.cpu().numpy(), ref.numpy()) <= 1e-5
+    assert torch.equal(kc[:, pos], k.view(kvh, hd)) and torch.equal(vc[:, pos], v.view(kvh, hd))
+    assert torch.equal(kc[:, :pos], K[:, :pos])  # nothing else changed
+
+
+def test_attention_decode_rejects_bad_args(gpu):
+    import littlebit_amd._lib as L
+    lib = L.load()
+    x = torch.zeros(1024, device=gpu)
+    p = x.data_ptr()
+    assert lib.lbk_attention_decode(p, p, p, p, p, 6, 4, 128, 64, None, 0, 1.0, p, 4096, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_decode(p, p, p, p, p, 4, 4, 96, 64, None, 0, 1.0, p, 4096, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_decode(p, p, p, p, p, 4, 4, 64, 64, None, 64, 1.0, p, 4096, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_decode(p, p, p, p, p, 4, 4, 64, 300, None, 0, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
 
 
 def test_batch_equals_token_by_token(gpu):

@@ -386,3 +386,54 @@ def test_op_precondition_errors(gpu):
     cpu_in[0] = cpu_in[0].cpu()
     with pytest.raises(RuntimeError, match="GPU"):
         littlebit_linear(*cpu_in)
+
+
+# --------------------------------------------------------------------------- fused inputs / residual
+def _fused_run(gpu, M, K, specs, mode, x_dtype=torch.float32, residual=False, seed=3400):
+    from littlebit_amd import LittleBitProjection, LittleBitProjectionGroup
+    x, projs = _group_case(seed + M, M, K, specs)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    group = LittleBitProjectionGroup([LittleBitProjection([_dev_branch(b, gpu) for b in brs]) for brs, _ in projs])
+    tx = torch.from_numpy(x).to(gpu).to(x_dtype)
+    kw = {}
+    if mode == "rms":
+        w = (1 + 0.2 * rng.standard_normal(K)).astype(np.float32)
+        kw = {"rms_weight": torch.from_numpy(w).to(gpu), "rms_eps": 1e-5}
+        xin = O.rms_norm(tx.float().cpu().numpy(), w, 1e-5)
+    else:
+        u = rng.standard_normal((M, K)).astype(np.float32)
+        tu = torch.from_numpy(u).to(gpu).to(x_dtype)
+        kw = {"x_up": tu}
+        xin = O.silu_mul(tx.float().cpu().numpy(), tu.float().cpu().numpy())
+    outs = res_np = None
+    if residual:
+        res_np = [rng.standard_normal((M, N)).astype(np.float32) * 50 for N, _ in specs]
+        outs = [torch.from_numpy(r).to(gpu) for r in res_np]
+        kw["residuals"] = outs  # in place: y aliases the residual
+    ys = group.forward(tx, outs=outs, out_dtype=torch.float32, **kw)
+    torch.cuda.synchronize()
+    tol = TOL_BF16_PREFILL if (x_dtype == torch.bfloat16 and M > 16) else TOL_F32
+    for i, ((brs, _), y) in enumerate(zip(projs, ys)):
+        ref = O.littlebit_forward(xin, brs, K, specs[i][0])
+        if residual:
+            ref = ref + res_np[i]
+        err = O.rel_err(y.cpu().numpy(), ref)
+        print(f"[fused] {mode} M={M} proj {i} rel_err={err:.2e}", flush=True)
+        assert err <= tol, (mode, M, i, err)
+
+
+@pytest.mark.parametrize("M", [1, 8, 16, 40])
+def test_fused_rmsnorm_group(gpu, M):
+    _fused_run(gpu, M, 4096, [(4096, [205, 1843]), (1024, [81])], "rms")
+
+
+@pytest.mark.parametrize("M,x_dtype", [(1, torch.float32), (8, torch.float32), (40, torch.float32),
+                                       (3, torch.bfloat16), (200, torch.bfloat16)])
+def test_fused_silu_mul(gpu, M, x_dtype):
+    _fused_run(gpu, M, 1000, [(300, [64, 130])], "silu", x_dtype=x_dtype)
+
+
+@pytest.mark.parametrize("M", [1, 8, 33])
+def test_residual_in_place(gpu, M):
+    _fused_run(gpu, M, 512, [(512, [45, 301]), (96, [9])], "rms", residual=True)
+    _fused_run(gpu, M, 1000, [(4096, [298])], "silu", residual=True)

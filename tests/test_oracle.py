@@ -206,3 +206,30 @@ def test_fuse_mid_is_exact_product_of_bf16():
 def test_rel_err_definition():
     assert O.rel_err(np.array([1.0, 2.0]), np.array([1.0, 4.0])) == pytest.approx(0.5)
     assert O.rel_err(np.zeros((0, 3)), np.zeros((0, 3))) == 0.0
+
+
+# --------------------------------------------------------------------------- fused inputs
+def test_rms_norm_closed_forms():
+    w = np.array([1.0, 2.0, -3.0, 0.5])
+    # a constant row c: mean(x^2) = c^2, so the output is c / sqrt(c^2 + eps) * w
+    for c in (2.0, -0.5):
+        x = np.full((1, 4), c)
+        np.testing.assert_allclose(O.rms_norm(x, w, 1e-6), c / np.sqrt(c * c + 1e-6) * w[None], rtol=1e-15)
+    # eps = 0: scale invariant, unit RMS
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 64))
+    np.testing.assert_allclose(O.rms_norm(7.5 * x, np.ones(64), 0.0), O.rms_norm(x, np.ones(64), 0.0), rtol=1e-12)
+    np.testing.assert_allclose(np.sqrt((O.rms_norm(x, np.ones(64), 0.0) ** 2).mean(-1)), 1.0, rtol=1e-12)
+    # torch's float64 RMSNorm agrees
+    tx = torch.from_numpy(x)
+    ref = torch.nn.functional.rms_norm(tx, (64,), torch.ones(64, dtype=torch.float64), eps=1e-5).numpy()
+    np.testing.assert_allclose(O.rms_norm(x, np.ones(64), 1e-5), ref, rtol=1e-12)
+
+
+def test_silu_mul_closed_forms():
+    assert O.silu_mul(0.0, 5.0) == 0.0
+    np.testing.assert_allclose(O.silu_mul(2.0, 3.0), 2.0 / (1.0 + np.exp(-2.0)) * 3.0, rtol=1e-15)
+    np.testing.assert_allclose(O.silu_mul(40.0, 1.0), 40.0, rtol=1e-15)  # sigmoid -> 1
+    assert abs(O.silu_mul(-40.0, 1.0)) < 1e-15
+    g = np.linspace(-6, 6, 25)
+    np.testing.assert_allclose(O.silu_mul(g, 1.0), torch.nn.functional.silu(torch.from_numpy(g)).numpy(), rtol=1e-12)
