@@ -664,17 +664,15 @@ __global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kerne
 // the precision of the reference's bf16 forward (littlebit.py:116-121).
 // Stages 1 and 2: block tile 128 (m) x 128 (columns: latent rows in stage
 // 1, outputs in stage 2), 4 waves of 64 x 64 (2 x 2 MFMA tiles), k-steps of
-// 64.  A tiles go to LDS by plain 16-byte copies, double-buffered; the +-1 B
-// operand is expanded in registers from the sign words of the lane's
-// column: for 16-k sub-step s, lane l (column l % 32, k 8*(l/32) .. +8 of
+// 64.  A tiles go from global memory straight to LDS through a 4-stage ring
+// (see gemm_mainloop); the +-1 B operand is expanded in registers from the
+// sign words of the lane's column: for 16-k sub-step s, lane l (column l % 32, k 8*(l/32) .. +8 of
 // the 32x32x16 operand) takes byte 2*(s%2) + l/32 of word s/2 of the step.
 // ---------------------------------------------------------------------------
 constexpr int kGB = 128;             // block tile (m and columns)
 constexpr int kGK = 64;              // k per step (two sign words per column)
 constexpr int kGThreads = 256;
 constexpr int kGChunks = kGB * kGK / 8 / kGThreads;  // 16-byte A chunks per thread per step
-constexpr int kGRow = kGK + 8;       // bf16 per LDS row: 144 B, 16-byte aligned, rows 36 banks apart
-constexpr int kGTile = kGB * kGRow;  // bf16 per LDS tile
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -791,86 +789,98 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
   }
 }
 
-// Rows [m0, m0 + 128) x k [k0, k0 + 64) of the bf16 planes of A (lda >= k0 +
-// 64): thread tid copies 16-byte chunks c = tid + 256 * j (row c / 8, k
-// 8 * (c % 8)).  load() issues the loads, store() writes LDS, so the loads
-// of the next step stay in flight across this step's MFMAs.  Rows past M
-// repeat row M - 1.
-template <bool SPLIT>
-struct AStage {
-  u32x4 raw[kGChunks][SPLIT ? 2 : 1];
-
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ A, int64_t plane, int64_t lda, int M, int m0,
-                                       int k0, int tid) {
-#pragma unroll
-    for (int j = 0; j < kGChunks; ++j) {
-      const int c = tid + kGThreads * j;
-      const int m = min(m0 + (c >> 3), M - 1);
-      const uint16_t* __restrict__ src = A + int64_t(m) * lda + k0 + 8 * (c & 7);
-      raw[j][0] = *reinterpret_cast<const u32x4*>(src);
-      if constexpr (SPLIT) raw[j][1] = *reinterpret_cast<const u32x4*>(src + plane);
-    }
-  }
-
-  __device__ __forceinline__ void store(unsigned short* lds, int tid) const {
-#pragma unroll
-    for (int j = 0; j < kGChunks; ++j) {
-      const int c = tid + kGThreads * j;
-      const int off = (c >> 3) * kGRow + 8 * (c & 7);
-      *reinterpret_cast<u32x4*>(lds + off) = raw[j][0];
-      if constexpr (SPLIT) *reinterpret_cast<u32x4*>(lds + kGTile + off) = raw[j][1];
-    }
-  }
-};
+// Encoding of s_waitcnt vmcnt(n) lgkmcnt(0) on gfx9 (expcnt left alone).
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
 
 // acc[i][j] += A[m0 + 64*wm + 32*i + .., :64*nks] . S[:64*nks, c0 + 64*wn + 32*j + ..]
 // S[k, c] = sign bit k of row c of W (ldw words per row, zero past it);
-// step ks reads words 2*ks and 2*ks + 1.  lds: two buffers of (SPLIT ? 2 : 1)
-// tiles.  Ends with a barrier.  (Loading two steps ahead instead of one
-// costs registers enough to halve the occupancy, which measured slower.)
+// step ks reads words 2*ks and 2*ks + 1.
+//
+// A tiles (128 rows x 64 k per plane, rows past M repeat row M - 1) go from
+// global memory straight to LDS (global_load_lds_dwordx4) through a ring of
+// kGStages stages, issued kGStages - 1 steps ahead; each stage is its own
+// __shared__ array so that the compiler can tell which load fills which
+// stage.  Rows are 128 bytes, 16-byte chunk c of row r stored at chunk
+// c ^ (r & 7), so the 32 rows a 32x32x16 operand reads fall in distinct
+// banks.  Each step issues the same loads (its sign words and its DMA) on
+// every path; before step ks every wave waits (vmcnt) until only the two
+// newer steps' loads are outstanding -- vector loads complete in order, so
+// its own loads of stage ks have landed -- and a barrier makes the whole
+// tile visible; the loads for step ks + 3 then go to the stage that step
+// ks - 1 read.  Ends with a barrier.
+constexpr int kGStages = 4;
+
 template <bool SPLIT>
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t plane, int64_t lda, int M,
                                               int m0, const uint32_t* __restrict__ W, int ldw, int ncols, int c0,
-                                              int nks, unsigned short* lds, f32x16 (&acc)[2][2], int tid) {
+                                              int nks, f32x16 (&acc)[2][2], int tid) {
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  typedef __attribute__((address_space(1))) void* glb_ptr_t;
   constexpr int NT = SPLIT ? 2 : 1;
+  constexpr int TILE = kGB * kGK;           // elements per plane per stage
+  constexpr int DMA_PER_STEP = 4 * NT;      // global_load_lds per wave per step
+  constexpr int WORDS_PER_STEP = 4;         // sign-word loads per lane per step
+  __shared__ __attribute__((aligned(16))) uint16_t st0[NT * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[NT * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t st2[NT * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t st3[NT * TILE];
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const uint32_t* __restrict__ wrow[2];
-  bool cv[2];
+  uint32_t cmask[2];  // all ones for a column inside the matrix
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = c0 + 64 * wn + 32 * j + lr;
-    cv[j] = col < ncols;
-    wrow[j] = W + int64_t(cv[j] ? col : 0) * ldw;
+    cmask[j] = col < ncols ? ~0u : 0u;
+    wrow[j] = W + int64_t(col < ncols ? col : 0) * ldw;
   }
+  // this lane's source rows and chunks for its 4 DMA slots of a stage
+  const uint16_t* src[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int slot = (wave * 4 + j) * 64 + lane;
+    const int row = slot >> 3, c = (slot & 7) ^ (row & 7);
+    src[j] = A + int64_t(min(m0 + row, M - 1)) * lda + 8 * c;
+  }
+  auto issue = [&](int ks, uint16_t* st) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint16_t* dst = st + (wave * 4 + j) * 512;
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + int64_t(ks) * kGK), (lds_ptr_t)dst, 16, 0, 0);
+      if constexpr (SPLIT)
+        __builtin_amdgcn_global_load_lds((glb_ptr_t)(src[j] + plane + int64_t(ks) * kGK), (lds_ptr_t)(dst + TILE), 16,
+                                         0, 0);
+    }
+  };
+  // Raw words at a clamped index: the loads are unconditional, so every step
+  // issues the same WORDS_PER_STEP + DMA loads on every path and the vmcnt
+  // waits below stay exact; compute() masks columns and words past the row
+  // when it uses them, three steps later (masking here would make the
+  // compiler wait for the loads at once).
   auto load_words = [&](int ks, uint32_t (&w)[2][2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int wi = 2 * ks + h;
-        w[j][h] = (cv[j] && wi < ldw) ? wrow[j][wi] : 0u;
-      }
+      for (int h = 0; h < 2; ++h) w[j][h] = wrow[j][min(2 * ks + h, ldw - 1)];
   };
-  AStage<SPLIT> st;
-  st.load(A, plane, lda, M, m0, 0, tid);
-  uint32_t w[2][2];
-  load_words(0, w);
-  st.store(lds, tid);
-  __syncthreads();
-
   uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
   asm volatile("" : "+v"(kmask), "+v"(kone));
-  for (int ks = 0; ks < nks; ++ks) {
-    const bool more = ks + 1 < nks;
-    uint32_t wnext[2][2] = {{0u, 0u}, {0u, 0u}};
-    if (more) {
-      st.load(A, plane, lda, M, m0, (ks + 1) * kGK, tid);
-      load_words(ks + 1, wnext);
+  auto compute = [&](int ks, const uint16_t* a, const uint32_t (&wraw)[2][2]) {
+    // the empty asm keeps the words' first use in this step, after its
+    // barrier, instead of letting the scheduler hoist the sign expansion to
+    // where the loads were just issued (which waits for them there)
+    uint32_t w[2][2];
+    const uint32_t hmask = 2 * ks + 1 < ldw ? ~0u : 0u;  // odd last word of a row
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      w[j][0] = wraw[j][0];
+      w[j][1] = wraw[j][1];
+      asm volatile("" : "+v"(w[j][0]), "+v"(w[j][1]));
+      w[j][0] &= cmask[j];
+      w[j][1] &= cmask[j] & hmask;
     }
-    const unsigned short* a = lds + (ks & 1) * NT * kGTile;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       bf16x8 b[2];
@@ -878,34 +888,68 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
       for (int j = 0; j < 2; ++j) b[j] = signs_to_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask, kone);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int off = (64 * wm + 32 * i + lr) * kGRow + 16 * s + 8 * lh;
+        const int r = 64 * wm + 32 * i + lr;
+        const int off = r * kGK + (((2 * s + lh) ^ (r & 7)) << 3);
         const bf16x8 ah = *reinterpret_cast<const bf16x8*>(a + off);
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b[j], acc[i][j], 0, 0, 0);
         if constexpr (SPLIT) {
-          const bf16x8 al = *reinterpret_cast<const bf16x8*>(a + kGTile + off);
+          const bf16x8 al = *reinterpret_cast<const bf16x8*>(a + TILE + off);
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b[j], acc[i][j], 0, 0, 0);
         }
       }
     }
-    if (more) {
-      st.store(lds + ((ks + 1) & 1) * NT * kGTile, tid);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        w[j][0] = wnext[j][0];
-        w[j][1] = wnext[j][1];
-      }
-    }
-    __syncthreads();
+  };
+  // Step ks reads stage `cur` and words wc; it refills `nxt` (read by step
+  // ks - 1) with step ks + 3 and wn with that step's words.  Past the last
+  // step the refill repeats step nks - 1 into a stage nothing reads again,
+  // so exactly two steps' loads are always newer than step ks's.
+  auto fill = [&](int ks, uint16_t* st, uint32_t (&w)[2][2]) {
+    const int kc = min(ks, nks - 1);
+    load_words(kc, w);
+    issue(kc, st);
+  };
+  // The memory clobbers keep LDS reads from being moved above the barrier;
+  // the waitcnt and the barrier also delimit the scheduler's regions, so
+  // step ks + 1 and ks + 2 issue all their loads after step ks's.
+  auto step = [&](int ks, const uint16_t* cur, uint32_t (&wc)[2][2], uint16_t* nxt, uint32_t (&wn)[2][2]) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * (DMA_PER_STEP + WORDS_PER_STEP)));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    fill(ks + 3, nxt, wn);
+    compute(ks, cur, wc);
+  };
+  uint32_t w0[2][2], w1[2][2], w2[2][2], w3[2][2];
+  fill(0, st0, w0);
+  __builtin_amdgcn_sched_barrier(0);
+  fill(1, st1, w1);
+  __builtin_amdgcn_sched_barrier(0);
+  fill(2, st2, w2);
+  __builtin_amdgcn_sched_barrier(0);
+  // whole rounds of the ring, then the remaining steps: every path into the
+  // loop header has issued the same loads
+  int ks = 0;
+  for (; ks + 4 <= nks; ks += 4) {
+    step(ks, st0, w0, st3, w3);
+    step(ks + 1, st1, w1, st0, w0);
+    step(ks + 2, st2, w2, st1, w1);
+    step(ks + 3, st3, w3, st2, w2);
   }
+  if (ks < nks) step(ks, st0, w0, st3, w3);
+  if (ks + 1 < nks) step(ks + 1, st1, w1, st0, w0);
+  if (ks + 2 < nks) step(ks + 2, st2, w2, st1, w1);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Stage 1.  grid = (m-tiles, column tiles of all segments), 256 threads.
 template <bool SPLIT>
 __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
   int si = 0;
@@ -920,7 +964,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-  gemm_mainloop<SPLIT>(p.a + S.abase, p.a_plane, p.Kp, p.M, m0, S.V, p.KW, S.R, c0, p.Kp / kGK, glds, acc, tid);
+  gemm_mainloop<SPLIT>(p.a + S.abase, p.a_plane, p.Kp, p.M, m0, S.V, p.KW, S.R, c0, p.Kp / kGK, acc, tid);
 
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -954,7 +998,6 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
 // Stage 2.  grid = (m-tiles, column tiles of all projections), 256 threads.
 template <typename YT, bool SPLIT>
 __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned short glds[];
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
   int pi = 0;
@@ -971,10 +1014,10 @@ __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
     for (int j = 0; j < 2; ++j) acc0[i][j] = acc1[i][j] = f32x16{};
   // T rows are zero from R to RP >= 64 * ceil(RW / 2), so whole 64-k steps are safe
   gemm_mainloop<SPLIT>(p.t + P.tbase[0], p.t_plane, P.RP[0], p.M, m0, P.U[0], P.RW[0], P.N, c0, (P.RW[0] + 1) / 2,
-                       glds, acc0, tid);
+                       acc0, tid);
   if (P.nb > 1)
     gemm_mainloop<SPLIT>(p.t + P.tbase[1], p.t_plane, P.RP[1], p.M, m0, P.U[1], P.RW[1], P.N, c0,
-                         (P.RW[1] + 1) / 2, glds, acc1, tid);
+                         (P.RW[1] + 1) / 2, acc1, tid);
 
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -1330,7 +1373,6 @@ size_t compact_rows(int mt, int64_t nch) {
   return size_t(mb) * size_t(nch) * size_t(2 * mr + 1);
 }
 
-size_t gemm_lds_bytes(bool split) { return size_t(2) * (split ? 2 : 1) * kGTile * sizeof(uint16_t); }
 
 // Elements per plane of the GEMM path's A (per segment [M][Kp]) and T (per
 // segment [M][RP]); planes are bf16, two of each with SPLIT.
@@ -1603,7 +1645,7 @@ int forward_gemm(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x
   p.xvec = xvec ? 1 : 0;
   const int64_t mtiles = ceil_div(M, kGB);
   if (nt1 > 65535 || nt2 > 65535) return set_error(LBK_ERR_ARG, "too many column tiles for the GEMM path");
-  const size_t lds = gemm_lds_bytes(split);
+  const size_t lds = 0;  // the stage ring is static LDS
   const dim3 g0{unsigned(M), unsigned(si), 1u};
   const dim3 g1{unsigned(mtiles), unsigned(nt1), 1u}, g2{unsigned(mtiles), unsigned(nt2), 1u};
   if (x_dtype == LBK_F32) hipLaunchKernelGGL((gemm_scale_kernel<float, true>), g0, dim3(kGThreads), 0, s, p);
