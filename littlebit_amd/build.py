@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -42,19 +43,63 @@ def hipcc_path() -> str:
     return found
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library; returns its path.  Always recompiles."""
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc_path(), *HIP_FLAGS, "-I", str(INCLUDE_DIR), str(SRC), "-o", str(tmp)]
+def inline_asm_instructions(asm: str) -> list:
+    """Instructions the device assembly holds inside inline asm blocks.
+
+    The library's inline asm only pins values in registers or orders memory
+    (empty blocks).  An instruction inside one is invisible to the compiler's
+    hazard recognizer: a VALU result written there and read by an MFMA gets no
+    wait states, which made MFMAs read stale operands on gfx950.  The build
+    refuses device code that has any.
+    """
+    bad, func, inside = [], "?", False
+    for line in asm.splitlines():
+        if line and not line[0].isspace() and line.startswith("_Z") and ":" in line:
+            func = line.split(":", 1)[0]
+        s = line.strip()
+        if s.startswith(";;#ASMSTART"):
+            inside = True
+        elif s.startswith(";;#ASMEND"):
+            inside = False
+        elif inside and s and not s.startswith(";"):
+            bad.append(f"{func}: {s}")
+    return bad
+
+
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def _finish(proc, what):
+    out, err = proc.communicate()
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    err = "\n".join(line for line in err.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}\n{proc.stdout}")
+        raise RuntimeError(f"hipcc ({what}) failed ({proc.returncode}):\n{err}\n{out}")
+    return err
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library and check its device code; returns its path.
+    Always recompiles.  The device assembly (for the inline asm check) is
+    compiled in parallel with the library."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    with tempfile.TemporaryDirectory() as td:
+        asm_path = Path(td) / "device.s"
+        lib_proc = _run([hipcc_path(), *HIP_FLAGS, "-I", str(INCLUDE_DIR), str(SRC), "-o", str(tmp)], verbose)
+        flags = [f for f in HIP_FLAGS if f != "-shared"]
+        asm_proc = _run([hipcc_path(), *flags, "--cuda-device-only", "-S", "-I", str(INCLUDE_DIR), str(SRC),
+                         "-o", str(asm_path)], verbose)
+        err = _finish(lib_proc, "library")
+        _finish(asm_proc, "device assembly")
+        bad = inline_asm_instructions(asm_path.read_text())
+    if bad:
+        tmp.unlink(missing_ok=True)
+        raise RuntimeError(f"{len(bad)} instructions inside inline asm, e.g.\n" + "\n".join(bad[:5]))
     if verbose and err.strip():
         print(err, file=sys.stderr)
     os.replace(tmp, LIB_PATH)

@@ -110,6 +110,36 @@ __device__ __forceinline__ void load8(const uint16_t* p, float (&a)[8]) {
   }
 }
 
+// 8 consecutive elements from a 16-byte aligned address, kept as loaded and
+// converted to float only by get(): a batch of Raw8 loads is issued before
+// any of it is waited for.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<float> {
+  float4 u, w;
+  __device__ __forceinline__ void load(const float* p) {
+    u = *reinterpret_cast<const float4*>(p);
+    w = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ __forceinline__ void get(float (&a)[8]) const {
+    a[0] = u.x; a[1] = u.y; a[2] = u.z; a[3] = u.w;
+    a[4] = w.x; a[5] = w.y; a[6] = w.z; a[7] = w.w;
+  }
+};
+template <>
+struct Raw8<uint16_t> {
+  u32x4 u;
+  __device__ __forceinline__ void load(const uint16_t* p) { u = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void get(float (&a)[8]) const {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      a[2 * d] = __uint_as_float(u[d] << 16);
+      a[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // MFMA path parameters
 // ---------------------------------------------------------------------------
@@ -153,6 +183,7 @@ struct MfmaParams {
   int M, K, KW;
   int tsize;    // M * sum(RP) floats
   int nkc;      // k-chunks
+  int splits;   // expand_mfma_kernel: waves sharing the rank steps of a 16-row tile
   int xvec;     // x (x1, rms weight) and every g allow 16-byte loads (aligned, K % 8 == 0)
   int xmode;    // LBK_INPUT_*: x as is, RMSNorm(x) * w, or SiLU(x) * x1
   const void* x;
@@ -174,13 +205,14 @@ struct MfmaParams {
 // Calls of any shape may follow each other on one workspace; graph replay
 // works because the state lives in device memory, not in kernel arguments.
 
-// v_and_or_b32 is VOP3, which takes no literal operands on gfx9: the masks
-// live in VGPRs (pinned by an empty asm so they are not re-materialised).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
-  return r;
-}
+// (x & m) | o, one v_and_or_b32.  That is VOP3, which takes no literal
+// operands on gfx9, so the callers keep the masks in VGPRs (pinned by an
+// empty asm so they are not re-materialised).  It must stay plain C: the
+// result feeds an MFMA, and the compiler inserts the wait states between a
+// VALU write and an MFMA read of the same register only for writes it can
+// see -- the same instruction written as inline asm let MFMAs read stale B
+// operands on gfx950 whenever the scheduler placed it right before them.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) { return (x & m) | o; }
 
 // Byte j of a sign word -> 8 bf16 (+1 for bit 0, -1 for bit 1); element i is
 // bit 8j+i.  Each dword holds elements 2d (low half) and 2d+1 (high half):
@@ -239,21 +271,11 @@ struct Compact {
 // decode step, patches/littlebit_cpu_optimized.cpp:1370-1438).
 __device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
 
-// rs[m] for m < M: every thread sums x[m, k]^2 over k = tid, tid + BLOCK, ..;
-// waves reduce by shuffles, then one LDS pass.  Ends with a barrier.
-template <typename XT, int MT, int BLOCK>
-__device__ __forceinline__ void rms_scales(const XT* __restrict__ x, int M, int K, float eps, float* rs,
+// rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) from per-thread partial sums of
+// squares: shuffles within each wave, then one LDS pass.  Ends with a barrier.
+template <int MT, int BLOCK>
+__device__ __forceinline__ void rms_finish(float (&part)[MT], int K, float eps, float* rs,
                                            float* scratch /* [BLOCK / 64][MT] */, int tid) {
-  float part[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) part[m] = 0.f;
-  for (int k = tid; k < K; k += BLOCK) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float v = m < M ? to_f32(x[size_t(m) * K + k]) : 0.f;
-      part[m] += v * v;
-    }
-  }
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
 #pragma unroll
@@ -270,6 +292,59 @@ __device__ __forceinline__ void rms_scales(const XT* __restrict__ x, int M, int 
     rs[tid] = 1.f / sqrtf(ssum / float(K) + eps);
   }
   __syncthreads();
+}
+
+// rs[m] for m < M, any alignment: every thread sums x[m, k]^2 over k = tid,
+// tid + BLOCK, ...  Ends with a barrier.
+template <typename XT, int MT, int BLOCK>
+__device__ __forceinline__ void rms_scales(const XT* __restrict__ x, int M, int K, float eps, float* rs,
+                                           float* scratch /* [BLOCK / 64][MT] */, int tid) {
+  float part[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) part[m] = 0.f;
+  for (int k = tid; k < K; k += BLOCK) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = m < M ? to_f32(x[size_t(m) * K + k]) : 0.f;
+      part[m] += v * v;
+    }
+  }
+  rms_finish<MT, BLOCK>(part, K, eps, rs, scratch, tid);
+}
+
+// Per-thread partial sums of x[m, k]^2 for m < MT (rows past M read row
+// M - 1; their scales are never used) over this thread's 8-element groups
+// k = 8 * (tid + BLOCK * j); rows 16-byte aligned, K % 8 == 0.  Rows go in
+// groups of up to 4, two 8-element groups of each in flight at clamped
+// addresses, so a row group costs one round trip when K <= 16 * BLOCK.
+template <typename XT, int MT, int BLOCK>
+__device__ __forceinline__ void sumsq_vec(const XT* __restrict__ x, int M, int K, float (&part)[MT], int tid) {
+  constexpr int RG = MT < 4 ? MT : 4;
+  const int K8 = K / 8;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) part[m] = 0.f;
+  for (int g0 = 0; g0 < K8; g0 += 2 * BLOCK) {
+#pragma unroll
+    for (int m0 = 0; m0 < MT; m0 += RG) {
+      Raw8<XT> r[RG][2];
+#pragma unroll
+      for (int i = 0; i < RG; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          r[i][j].load(x + size_t(min(m0 + i, M - 1)) * K + 8 * min(g0 + tid + BLOCK * j, K8 - 1));
+#pragma unroll
+      for (int i = 0; i < RG; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float a[8];
+          r[i][j].get(a);
+          float s = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s += a[e] * a[e];
+          part[m0 + i] += g0 + tid + BLOCK * j < K8 ? s : 0.f;
+        }
+    }
+  }
 }
 
 // 8 effective inputs (m, kb .. kb+7) times g, zeros past K.
@@ -347,6 +422,100 @@ __device__ __forceinline__ void build_compact(u32x4* lds, int nch, int M, int ti
   }
 }
 
+// Effective input (times g) of the 8 k from kb of every stored row of the
+// compact A operand, input mode MODE, vector path (x, x1, g and the RMSNorm
+// weight 16-byte aligned, K % 8 == 0: a chunk lies wholly inside K or wholly
+// past it).  load() issues every load at clamped addresses; get() computes
+// what load_input8 computes, in the same order, zero past K.
+template <typename XT, int MT, int MODE>
+struct InputChunk {
+  using L = Compact<MT>;
+  static constexpr bool kSilu = MODE == LBK_INPUT_SILU_MUL;
+  Raw8<XT> xr[L::MB][L::MR];
+  Raw8<XT> ur[kSilu ? L::MB : 1][kSilu ? L::MR : 1];
+  Raw8<float> gr, wr;
+  bool valid;
+
+  __device__ __forceinline__ void load(const MfmaParams& p, const float* __restrict__ g, int kb) {
+    valid = kb < p.K;
+    const int kl = valid ? kb : 0;
+    const XT* __restrict__ x = static_cast<const XT*>(p.x);
+    gr.load(g + kl);
+    if constexpr (MODE == LBK_INPUT_RMSNORM) wr.load(p.nw + kl);
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) {
+        const size_t at = size_t(min(mb * 8 + ml, p.M - 1)) * p.K + kl;
+        xr[mb][ml].load(x + at);
+        if constexpr (kSilu) ur[mb][ml].load(static_cast<const XT*>(p.x1) + at);
+      }
+  }
+
+  __device__ __forceinline__ void get(int mb, int ml, float rsm, float (&a)[8]) const {
+    float gv[8];
+    gr.get(gv);
+    xr[mb][ml].get(a);
+    if constexpr (MODE == LBK_INPUT_RMSNORM) {
+      float wv[8];
+      wr.get(wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) gv[i] *= wv[i] * rsm;
+    } else if constexpr (kSilu) {
+      float uv[8];
+      ur[mb][ml].get(uv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = silu_f(a[i]) * uv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = valid ? a[i] * gv[i] : 0.f;
+  }
+};
+
+// The latent kernel's compact A operand of one k-chunk (NCH chunks of 8 k
+// from k0), vector path: thread tid < NCH owns chunk tid.  The chunk's loads
+// and, for RMSNorm, the loads of every row's sums of squares are all issued
+// before the first wait.  Ends with this thread's LDS writes, no barrier.
+template <typename XT, int MT, int NCH, int MODE>
+__device__ __forceinline__ void stage_latent_vec(const MfmaParams& p, const float* __restrict__ g, int k0,
+                                                 u32x4* lds, int tid) {
+  using L = Compact<MT>;
+  static_assert(NCH <= kBlock, "one chunk per thread");
+  const int c = min(tid, NCH - 1);
+  InputChunk<XT, MT, MODE> in;
+  in.load(p, g, k0 + 8 * c);
+  float rsv[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
+  if constexpr (MODE == LBK_INPUT_RMSNORM) {
+    __shared__ float rs[MT];
+    __shared__ float scratch[kBlock / 64 * MT];
+    float part[MT];
+    sumsq_vec<XT, MT, kBlock>(static_cast<const XT*>(p.x), p.M, p.K, part, tid);
+    rms_finish<MT, kBlock>(part, p.K, p.eps, rs, scratch, tid);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) rsv[m] = rs[m];
+  }
+  if (tid < NCH) {
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb) {
+      u32x4* base = lds + (size_t(mb) * NCH + c) * L::ROWS;
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) {
+        u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+        if (mb * 8 + ml < p.M) {
+          float a[8];
+          in.get(mb, ml, rsv[mb * 8 + ml], a);
+          split8(a, hi, lo);
+        }
+        base[ml] = hi;
+        base[L::MR + ml] = lo;
+      }
+      base[2 * L::MR] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Stage 1 (MFMA): t += l * (V_sign . (g*x)) over this block's k-chunk
 // grid.x = (row-blocks of all segments) * nkc, block = 256 threads (4 waves)
@@ -392,17 +561,18 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   const int r = rb * kRowBlock + wave * 16 + col;
   const int w0 = kc * (KC / 32) + grp * WPL;
 
-  // sign words first, so that their latency overlaps the A-operand build
+  // Sign words first, so that their latency overlaps the A-operand build.
+  // Every load is issued on every path (clamped addresses: rows past R are
+  // never stored, and words past the row meet A columns past K, which are
+  // zero), so that no wait has to cover a path that skipped a load.
   uint32_t words[WPL];
   {
     const uint32_t* __restrict__ vrow = V + size_t(r < R ? r : 0) * p.KW;
 #pragma unroll
-    for (int s = 0; s < WPL; ++s) {
-      const int w = w0 + s;
-      words[s] = (r < R && w < p.KW) ? vrow[w] : 0u;
-    }
+    for (int s = 0; s < WPL; ++s) words[s] = vrow[min(w0 + s, p.KW - 1)];
   }
-  const float lr = (r < R) ? lvec[r] : 0.f;
+  const float lv = lvec[min(r, R - 1)];
+  const float lr = r < R ? lv : 0.f;
   // Latent-buffer state.  Plain loads: within this launch only block 0
   // writes sync[1] and sync[2 + h], which no block of it reads.
   const uint32_t h = p.sync[0] & 1u;
@@ -410,14 +580,20 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   const uint32_t s1 = p.sync[3];
 
   // ---- A operand: hi/lo bf16 of g[k] * input[m, k] for this k-chunk ----
-  __shared__ float rs[MT];
-  if (p.xmode == LBK_INPUT_RMSNORM) {
-    __shared__ float rscratch[kBlock / 64 * MT];
-    rms_scales<XT, MT, kBlock>(static_cast<const XT*>(p.x), p.M, p.K, p.eps, rs, rscratch, tid);
+  if (p.xvec) {
+    if (p.xmode == LBK_INPUT_RMSNORM) stage_latent_vec<XT, MT, NCH, LBK_INPUT_RMSNORM>(p, g, k0, lds_a, tid);
+    else if (p.xmode == LBK_INPUT_SILU_MUL) stage_latent_vec<XT, MT, NCH, LBK_INPUT_SILU_MUL>(p, g, k0, lds_a, tid);
+    else stage_latent_vec<XT, MT, NCH, LBK_INPUT_PLAIN>(p, g, k0, lds_a, tid);
+  } else {
+    __shared__ float rs[MT];
+    if (p.xmode == LBK_INPUT_RMSNORM) {
+      __shared__ float rscratch[kBlock / 64 * MT];
+      rms_scales<XT, MT, kBlock>(static_cast<const XT*>(p.x), p.M, p.K, p.eps, rs, rscratch, tid);
+    }
+    build_compact<MT, kBlock>(lds_a, NCH, p.M, tid, [&](int c, int m, float (&a)[8]) {
+      load_input8<XT>(p, g, m, k0 + 8 * c, p.xmode == LBK_INPUT_RMSNORM ? rs[m] : 1.f, a);
+    });
   }
-  build_compact<MT, kBlock>(lds_a, NCH, p.M, tid, [&](int c, int m, float (&a)[8]) {
-    load_input8<XT>(p, g, m, k0 + 8 * c, p.xmode == LBK_INPUT_RMSNORM ? rs[m] : 1.f, a);
-  });
   __syncthreads();
 
   uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
@@ -478,100 +654,148 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b) per projection
-// block = 2 * TILES waves covering 16 * TILES output rows of one projection:
-// wave w owns tile w % TILES (16 rows) and half w / TILES of the rank steps
-// (4 sign words of a row) of both branches; the two halves meet in LDS.
-// Every block stages all of its projection's t, so the host picks TILES (2,
-// 4 or 8) to need the fewest rounds of blocks on the CUs that the LDS size
-// allows, then the fewest staging passes, then the most blocks.
-// grid.x = sum over projections of ceil(N / (16 * TILES))
+// Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b) [+ residual] per
+// projection.  block = WAVES waves over 16 * tiles output rows of one
+// projection, tiles = WAVES / splits: wave w owns row tile w % tiles and part
+// w / tiles of the rank steps (4 sign words of a row) of both branches taken
+// in sequence; the splits parts of a tile meet in LDS.  Every block stages all
+// of its projection's t.  The host picks WAVES and splits.
+// grid.x = sum over projections of ceil(N / (16 * tiles))
 // LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
+//
+// Every load the block needs -- the first staging chunk of each thread, the
+// sign words, h, bias and residual -- is issued before the first wait, at
+// clamped addresses so that no path skips a load: rows past N are never
+// stored, and sign words past a row meet ranks past R, whose t is zero.
 // ---------------------------------------------------------------------------
-template <int TILES_>
-struct ExpandShape {
-  static constexpr int TILES = TILES_;
-  static constexpr int THREADS = 2 * TILES * kWave;
-  static constexpr int ROWS = 16 * TILES;
-};
-
-template <typename YT, int MT, int S, int TILES>
-__global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kernel(MfmaParams p) {
+template <typename YT, int MT, int S, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p) {
   using L = Compact<MT>;
-  using E = ExpandShape<TILES>;
+  constexpr int THREADS = WAVES * kWave;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   u32x4* lds_t = reinterpret_cast<u32x4*>(lds_raw);
-  __shared__ float red[E::TILES][L::MB * 4][32];
+  __shared__ float red[WAVES][L::MB * 4][32];
   const int tid = int(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   const int lane = tid % kWave;
-  const int tile = wave % E::TILES;
-  const int half = wave / E::TILES;
   const int col = lane & 15;
   const int grp = lane >> 4;
+  const int splits = p.splits;
+  const int tiles = WAVES / splits;
+  const int tile = wave % tiles;
+  const int part = wave / tiles;
   int pi = 0;
 #pragma unroll
   for (int i = 1; i < kMaxProj; ++i) pi += (i < p.nproj && int(blockIdx.x) >= p.proj[i].tile0) ? 1 : 0;
   pi = __builtin_amdgcn_readfirstlane(pi);
   const ExpProj& P = p.proj[pi];
-  const int n = (int(blockIdx.x) - P.tile0) * E::ROWS + tile * 16 + col;
+  const int n = (int(blockIdx.x) - P.tile0) * 16 * tiles + tile * 16 + col;
+  const bool nvalid = n < P.N;
+  const int nc = nvalid ? n : 0;
+  const int M = p.M;
+  const bool two = P.nb > 1;
   // half of the latent buffer the latent kernel of this call filled; only
   // block 0 writes the state here, and only sync[0]
   const uint32_t hq = p.sync[1] & 1u;
-  const bool nvalid = n < P.N;
 
-  // this wave's steps: branch 0 steps [a0, a0 + n0), branch 1 steps [c0, c0 + n1)
+  // this wave's steps [q0, q1) of the branches in sequence: n0 steps of
+  // branch 0 from step q0, then n1 steps of branch 1 from its step c1
   const int steps0 = P.RWp[0] / 4;
-  const int steps = steps0 + (P.nb > 1 ? P.RWp[1] / 4 : 0);
-  const int split = (steps + 1) / 2;
-  const int q0 = half ? split : 0;
-  const int q1 = half ? steps : split;
-  const int a0 = q0;
+  const int steps = steps0 + (two ? P.RWp[1] / 4 : 0);
+  const int per = (steps + splits - 1) / splits;
+  const int q0 = min(part * per, steps);
+  const int q1 = min(q0 + per, steps);
   const int n0 = max(min(q1, steps0) - q0, 0);
-  const int c0 = max(q0, steps0) - steps0;
+  const int c1 = max(q0, steps0) - steps0;
   const int n1 = max(q1 - max(q0, steps0), 0);
 
-  // Sign words of the wave, unrolled over the compile-time bound S (>= n0,
-  // n1, chosen by the host), so every load is issued before the first use
-  // waits on any of them.  Every element is written on every path.
-  uint32_t pre0[S], pre1[S];
-  {
-    const int RW0 = P.RW[0];
-    const int w0 = 4 * a0 + grp;
-    const uint32_t* __restrict__ u0 = P.U[0] + size_t(nvalid ? n : 0) * RW0 + w0;
-    const int lim0 = nvalid ? RW0 - w0 : 0;  // words of this lane left in the row
-#pragma unroll
-    for (int i = 0; i < S; ++i) pre0[i] = (i < n0 && 4 * i < lim0) ? u0[4 * i] : 0u;
-    const int RW1 = P.nb > 1 ? P.RW[1] : 0;
-    const int w1 = 4 * c0 + grp;
-    const uint32_t* __restrict__ u1 = P.nb > 1 ? P.U[1] + size_t(nvalid ? n : 0) * RW1 + w1 : u0;
-    const int lim1 = (nvalid && P.nb > 1) ? RW1 - w1 : 0;
-#pragma unroll
-    for (int i = 0; i < S; ++i) pre1[i] = (i < n1 && 4 * i < lim1) ? u1[4 * i] : 0u;
-  }
-
+  // (1) this thread's first staging chunk: chunk q of the chunks of both
+  // branches in sequence, every stored row
   const int nch0 = 4 * P.RWp[0];
-  const int nch1 = P.nb > 1 ? 4 * P.RWp[1] : 0;
+  const int nch1 = two ? 4 * P.RWp[1] : 0;
+  const int nch = nch0 + nch1;
+  const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
   u32x4* tb0 = lds_t;
   u32x4* tb1 = lds_t + size_t(L::MB) * nch0 * L::ROWS;
-  {
-    const int M = p.M;
-    const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
-    const float* __restrict__ t0 = ta + P.tbase[0];
-    const int RP0 = P.RP[0];
-    build_compact<MT, E::THREADS>(tb0, nch0, M, tid, [&](int c, int m, float (&a)[8]) {
-      load8(t0 + size_t(m) * RP0 + 8 * c, a);
-    });
-    if (P.nb > 1) {
-      const float* __restrict__ t1 = ta + P.tbase[1];
-      const int RP1 = P.RP[1];
-      build_compact<MT, E::THREADS>(tb1, nch1, M, tid, [&](int c, int m, float (&a)[8]) {
-        load8(t1 + size_t(m) * RP1 + 8 * c, a);
-      });
+  // branch fields in scalar registers: a per-lane choice between two fields
+  // of the kernel arguments would otherwise become a vector load of the
+  // argument block, which every chunk load then waits for
+  const int tbase0 = __builtin_amdgcn_readfirstlane(P.tbase[0]);
+  const int tbase1 = __builtin_amdgcn_readfirstlane(P.tbase[1]);
+  const int rp0 = __builtin_amdgcn_readfirstlane(P.RP[0]);
+  const int rp1 = __builtin_amdgcn_readfirstlane(P.RP[1]);
+  auto load_chunk = [&](int q, Raw8<float> (&v)[L::MB][L::MR]) {
+    const bool b1 = q >= nch0;
+    const float* __restrict__ src = ta + (b1 ? tbase1 + 8 * (q - nch0) : tbase0 + 8 * q);
+    const int rp = b1 ? rp1 : rp0;
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) v[mb][ml].load(src + size_t(min(mb * 8 + ml, M - 1)) * rp);
+  };
+  auto put_chunk = [&](int q, const Raw8<float> (&v)[L::MB][L::MR]) {
+    const bool b1 = q >= nch0;
+    const int c = b1 ? q - nch0 : q;
+    u32x4* base0 = b1 ? tb1 : tb0;
+    const int nchb = b1 ? nch1 : nch0;
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb) {
+      u32x4* base = base0 + (size_t(mb) * nchb + c) * L::ROWS;
+#pragma unroll
+      for (int ml = 0; ml < L::MR; ++ml) {
+        u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+        if (mb * 8 + ml < M) {
+          float a[8];
+          v[mb][ml].get(a);
+          split8(a, hi, lo);
+        }
+        base[ml] = hi;
+        base[L::MR + ml] = lo;
+      }
+      base[2 * L::MR] = u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  Raw8<float> v[L::MB][L::MR];
+  load_chunk(min(tid, nch - 1), v);
+
+  // (2) sign words of the wave's steps: pre0[i] of branch 0 step q0 + i,
+  // pre1[i] of branch 1 step c1 + i
+  uint32_t pre0[S], pre1[S];
+  {
+    const int rw0 = P.RW[0], rw1 = two ? P.RW[1] : P.RW[0];
+    const uint32_t* __restrict__ r0 = P.U[0] + size_t(nc) * rw0;
+    const uint32_t* __restrict__ r1 = two ? P.U[1] + size_t(nc) * rw1 : r0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      pre0[i] = r0[min(4 * (q0 + i) + grp, rw0 - 1)];
+      pre1[i] = r1[min(4 * (c1 + i) + grp, rw1 - 1)];
+    }
+  }
+  // (3) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
+  const float h0v = P.h[0][nc];
+  const float h1v = P.h[two ? 1 : 0][nc];
+  const float* __restrict__ bsrc = P.bias ? P.bias : P.h[0];
+  const float bnv = bsrc[nc];
+  const float* __restrict__ rsrc = P.res ? P.res : P.h[0];
+  const size_t rstride = P.res ? size_t(P.N) : 0;  // no residual: every load reads h[0][0]
+  const int rcol = P.res ? nc : 0;
+  float resv[L::MB][4];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      resv[mb][i] = rsrc[size_t(min(mb * 8 + (grp & 1) * 4 + i, M - 1)) * rstride + rcol];
+
+  // (4) staging: the first chunk (waits for its loads only), then any chunks
+  // past the first THREADS
+  if (tid < nch) put_chunk(tid, v);
+  for (int q = tid + THREADS; q < nch; q += THREADS) {
+    load_chunk(q, v);
+    put_chunk(q, v);
   }
   __syncthreads();
 
+  // (5) MFMA over the wave's steps, branch 0 then branch 1
   uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
   asm volatile("" : "+v"(kmask), "+v"(kone));
   const int lrow = L::lane_row(col);
@@ -584,7 +808,7 @@ __global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kerne
 #pragma unroll
   for (int i = 0; i < S; ++i) {
     if (i >= n0) continue;
-    const int w = 4 * (a0 + i) + grp;
+    const int w = 4 * (q0 + i) + grp;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 bop = signs_to_bf16x8(pre0[i], j, kmask, kone);
@@ -598,7 +822,7 @@ __global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kerne
 #pragma unroll
   for (int i = 0; i < S; ++i) {
     if (i >= n1) continue;
-    const int w = 4 * (c0 + i) + grp;
+    const int w = 4 * (c1 + i) + grp;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 bop = signs_to_bf16x8(pre1[i], j, kmask, kone);
@@ -609,39 +833,44 @@ __global__ __launch_bounds__(ExpandShape<TILES>::THREADS) void expand_mfma_kerne
       }
     }
   }
-
-  // h-weighted branch sum of this half; C rows 4*grp + i (grp 0,1 hi, 2,3 lo)
-  const float h0 = nvalid ? P.h[0][n] : 0.f;
-  const float h1 = (nvalid && P.nb > 1) ? P.h[1][n] : 0.f;
+  // h-weighted branch sums; C rows 4*grp + i (grp 0,1 hi, 2,3 lo of the same m)
+  const float h1 = two ? h1v : 0.f;
   float out[L::MB][4];
 #pragma unroll
   for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      out[mb][i] = h0 * (acc0[mb][i] + __shfl_xor(acc0[mb][i], 32)) +
+      out[mb][i] = h0v * (acc0[mb][i] + __shfl_xor(acc0[mb][i], 32)) +
                    h1 * (acc1[mb][i] + __shfl_xor(acc1[mb][i], 32));
 
-  if (half == 1 && lane < 32) {
+  // (6) the other parts of the tile add theirs through LDS
+  if (splits > 1) {
+    if (part > 0 && lane < 32) {
 #pragma unroll
-    for (int mb = 0; mb < L::MB; ++mb)
+      for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[tile][mb * 4 + i][lane] = out[mb][i];
+        for (int i = 0; i < 4; ++i) red[wave][mb * 4 + i][lane] = out[mb][i];
+    }
+    __syncthreads();
+    if (part == 0) {
+      for (int s = 1; s < splits; ++s) {
+#pragma unroll
+        for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[mb][i] += red[tile + s * tiles][mb * 4 + i][lane & 31];
+      }
+    }
   }
-  __syncthreads();
-  if (half == 0 && lane < 32 && nvalid) {
-    const float bn = P.bias ? P.bias[n] : 0.f;
+  if (part == 0 && lane < 32 && nvalid) {
+    const float bn = P.bias ? bnv : 0.f;
     YT* y = static_cast<YT*>(P.y);
-    const float* res = P.res;
     const int N = P.N;
 #pragma unroll
     for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = mb * 8 + grp * 4 + i;
-        if (m < p.M) {
-          const size_t o = size_t(m) * N + n;
-          store_out(y, o, out[mb][i] + red[tile][mb * 4 + i][lane] + bn + (res ? res[o] : 0.f));
-        }
+        if (m < M) store_out(y, size_t(m) * N + n, out[mb][i] + bn + (P.res ? resv[mb][i] : 0.f));
       }
   }
 
@@ -1360,7 +1589,8 @@ struct Plan {
   int nkc;       // k-chunks
   int nrb;       // row-blocks over all segments
   int wsteps;    // expand_mfma_kernel unroll bound S
-  int tiles;     // expand_mfma_kernel 16-row tiles per block
+  int waves;     // expand_mfma_kernel waves per block (4 or 8)
+  int splits;    // expand_mfma_kernel waves per 16-row tile
   size_t lds1, lds2;
   size_t ws_total;
 };
@@ -1394,28 +1624,45 @@ size_t gemm_ws_bytes(const ProjDesc* pd, int np, int64_t M, int64_t K, bool spli
 }
 
 // Static LDS of expand_mfma_kernel (the `red` array).
-size_t expand_static_lds(int tiles, int mt) { return size_t(tiles) * ((mt + 7) / 8) * 4 * 32 * sizeof(float); }
+size_t expand_static_lds(int waves, int mt) { return size_t(waves) * ((mt + 7) / 8) * 4 * 32 * sizeof(float); }
 
-// Rows per expand block: fewest rounds of blocks on 256 CUs (blocks per CU
-// bounded by LDS and by 2048 threads), then fewest passes of the t staging
-// loop (chunks per thread), then the most blocks.  0 if no shape fits in
-// the 160 KB of LDS.
-int expand_tiles(const ProjDesc* pd, int np, int mt, size_t lds2, int64_t chunks) {
+struct ExpandChoice {
+  int waves = 0, splits = 0, ws = 0;  // waves 0: no shape fits
+};
+
+// Expand launch shape: waves per block (4, 8 or 16) and waves per 16-row tile
+// (splits), by an estimate of the kernel's critical path in rank steps of one
+// wave: every pass of the t staging (a round trip to L2) weighs 8 steps and
+// repeats for each round of blocks the CUs cannot hold at once (blocks per
+// CU bounded by LDS and by 2048 threads); the busiest SIMD then runs
+// ceil(blocks / 256) * waves / 4 waves of ceil(steps / splits) steps each.
+// Ties go to fewer blocks (less staging traffic).
+ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64_t chunks, int64_t steps) {
   constexpr int kCUs = 256;
-  int best = 0;
-  int64_t best_key[3] = {INT64_MAX, INT64_MAX, INT64_MAX};
-  for (int t : {2, 4, 8}) {
-    if (t == 8 && mt < 4) continue;
-    const int threads = 2 * t * kWave;
-    const size_t lds = lds2 + expand_static_lds(t, mt);
+  ExpandChoice best;
+  int64_t best_key[2] = {INT64_MAX, INT64_MAX};
+  const int64_t mb = (mt + 7) / 8;
+  for (int waves : {4, 8, 16}) {
+    if (waves == 16 && mt > 8) continue;  // the staging registers of two m-blocks need more than 128 VGPRs
+    const int threads = waves * kWave;
+    const size_t lds = lds2 + expand_static_lds(waves, mt);
     if (lds > size_t(kMaxBlockLds)) continue;
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(int64_t(kLdsPerCU) / int64_t(lds), 2048 / threads));
-    int64_t blocks = 0;
-    for (int q = 0; q < np; ++q) blocks += ceil_div(pd[q].N, 16 * t);
-    const int64_t key[3] = {ceil_div(blocks, kCUs * per_cu), ceil_div(chunks, threads), -blocks};
-    if (std::lexicographical_compare(key, key + 3, best_key, best_key + 3)) {
-      best = t;
-      std::copy(key, key + 3, best_key);
+    for (int splits = 1; splits <= waves; splits *= 2) {
+      const int64_t ws = ceil_div(steps, splits);
+      if (ws > kMaxWaveSteps || (waves == 16 && ws > 16)) continue;  // 16 waves: 128 VGPRs hold 16 steps' words
+      const int tiles = waves / splits;
+      int64_t blocks = 0;
+      for (int q = 0; q < np; ++q) blocks += ceil_div(pd[q].N, 16 * tiles);
+      const int64_t rounds = ceil_div(blocks, kCUs * per_cu);
+      const int64_t cost = rounds * ceil_div(chunks, threads) * 8 + ceil_div(blocks, kCUs) * (waves / 4) * ws * mb;
+      const int64_t key[2] = {cost, blocks};
+      if (std::lexicographical_compare(key, key + 2, best_key, best_key + 2)) {
+        best.waves = waves;
+        best.splits = splits;
+        best.ws = int(ws);
+        std::copy(key, key + 2, best_key);
+      }
     }
   }
   return best;
@@ -1436,12 +1683,11 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     const size_t l2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
     if (4 * rwp_sum > chunks_max) chunks_max = 4 * rwp_sum;
     if (l2 > lds2) lds2 = l2;
-    const int64_t ws = (rwp_sum / 4 + 1) / 2;  // rank steps of the busier expand wave
-    if (ws > steps_max) steps_max = ws;
+    if (rwp_sum / 4 > steps_max) steps_max = rwp_sum / 4;  // rank steps of the projection
   }
   pl.nrb = int(nrb);
-  pl.mfma = (M >= 1 && M <= kMaxMfmaM && steps_max <= kMaxWaveSteps &&
-             expand_tiles(pd, np, pl.mt, lds2, chunks_max) > 0);
+  const ExpandChoice ex = expand_shape(pd, np, pl.mt, lds2, chunks_max, steps_max);
+  pl.mfma = M >= 1 && M <= kMaxMfmaM && ex.waves > 0;
   if (pl.mfma) {
     // enough blocks to cover the CUs, short per-wave chains
     pl.wpl = 2;
@@ -1449,10 +1695,11 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
       if (nrb * ceil_div(K, 128 * w) >= 256) { pl.wpl = w; break; }
     }
     pl.nkc = int(ceil_div(K, 128 * pl.wpl));
-    pl.wsteps = steps_max <= 4 ? 4 : steps_max <= 8 ? 8 : steps_max <= 16 ? 16 : 24;
+    pl.wsteps = ex.ws <= 4 ? 4 : ex.ws <= 8 ? 8 : ex.ws <= 16 ? 16 : kMaxWaveSteps;
     pl.lds1 = compact_rows(pl.mt, 128 * pl.wpl / 8) * 16;
     pl.lds2 = lds2;
-    pl.tiles = expand_tiles(pd, np, pl.mt, lds2, chunks_max);
+    pl.waves = ex.waves;
+    pl.splits = ex.splits;
     pl.ws_total = kTOffset + kTBytes;
   } else {
     pl.ws_total = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
@@ -1485,28 +1732,27 @@ void dispatch_latent(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
   }
 }
 
-template <typename YT, int MT, int S, int TILES>
+template <typename YT, int MT, int S, int WAVES>
 void launch_expand_mfma(const MfmaParams& p, int grid, size_t lds, hipStream_t s) {
-  using E = ExpandShape<TILES>;
-  hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S, TILES>), dim3(grid), dim3(E::THREADS), lds, s, p);
+  hipLaunchKernelGGL((expand_mfma_kernel<YT, MT, S, WAVES>), dim3(grid), dim3(WAVES * kWave), lds, s, p);
 }
 
 template <typename YT, int MT, int S>
-void dispatch_expand_tiles(const MfmaParams& p, int tiles, int grid, size_t lds, hipStream_t s) {
-  if constexpr (MT >= 4) {
-    if (tiles == 8) return launch_expand_mfma<YT, MT, S, 8>(p, grid, lds, s);
+void dispatch_expand_waves(const MfmaParams& p, int waves, int grid, size_t lds, hipStream_t s) {
+  if constexpr (MT <= 8 && S <= 16) {
+    if (waves == 16) return launch_expand_mfma<YT, MT, S, 16>(p, grid, lds, s);
   }
-  if (tiles == 4) return launch_expand_mfma<YT, MT, S, 4>(p, grid, lds, s);
-  launch_expand_mfma<YT, MT, S, 2>(p, grid, lds, s);
+  if (waves == 8) launch_expand_mfma<YT, MT, S, 8>(p, grid, lds, s);
+  else launch_expand_mfma<YT, MT, S, 4>(p, grid, lds, s);
 }
 
 template <typename YT, int MT>
 void dispatch_expand_s(const MfmaParams& p, const Plan& pl, int grid, hipStream_t s) {
   switch (pl.wsteps) {
-    case 4: dispatch_expand_tiles<YT, MT, 4>(p, pl.tiles, grid, pl.lds2, s); break;
-    case 8: dispatch_expand_tiles<YT, MT, 8>(p, pl.tiles, grid, pl.lds2, s); break;
-    case 16: dispatch_expand_tiles<YT, MT, 16>(p, pl.tiles, grid, pl.lds2, s); break;
-    default: dispatch_expand_tiles<YT, MT, kMaxWaveSteps>(p, pl.tiles, grid, pl.lds2, s); break;
+    case 4: dispatch_expand_waves<YT, MT, 4>(p, pl.waves, grid, pl.lds2, s); break;
+    case 8: dispatch_expand_waves<YT, MT, 8>(p, pl.waves, grid, pl.lds2, s); break;
+    case 16: dispatch_expand_waves<YT, MT, 16>(p, pl.waves, grid, pl.lds2, s); break;
+    default: dispatch_expand_waves<YT, MT, kMaxWaveSteps>(p, pl.waves, grid, pl.lds2, s); break;
   }
 }
 
@@ -1523,10 +1769,11 @@ void dispatch_expand(const MfmaParams& p, const Plan& pl, int grid, hipStream_t 
 
 int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
                  const InputDesc& in, int y_dtype, void* workspace, hipStream_t s) {
-  const int rows = 16 * pl.tiles;
+  const int rows = 16 * (pl.waves / pl.splits);
   MfmaParams p;
   memset(&p, 0, sizeof(p));
   p.nproj = np;
+  p.splits = pl.splits;
   p.M = int(M);
   p.K = int(K);
   p.KW = int(ceil_div(K, 32));
