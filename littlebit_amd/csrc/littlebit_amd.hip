@@ -185,6 +185,7 @@ struct MfmaParams {
   int nkc;      // k-chunks
   int splits;   // expand_mfma_kernel: waves sharing the rank steps of a 16-row tile
   int xvec;     // x (x1, rms weight) and every g allow 16-byte loads (aligned, K % 8 == 0)
+  int wvec;     // V rows allow WPL-word vector loads (16-byte aligned rows, KW % max(WPL, 4) == 0)
   int xmode;    // LBK_INPUT_*: x as is, RMSNorm(x) * w, or SiLU(x) * x1
   const void* x;
   const void* x1;       // second input of LBK_INPUT_SILU_MUL
@@ -568,8 +569,28 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   uint32_t words[WPL];
   {
     const uint32_t* __restrict__ vrow = V + size_t(r < R ? r : 0) * p.KW;
+    if (p.wvec) {
+      // the lane's WPL words in one or two vector loads: with KW % WPL == 0 a
+      // lane's words lie wholly inside the row or wholly past it
+      const uint32_t* __restrict__ src = vrow + (w0 < p.KW ? w0 : 0);
+      if constexpr (WPL == 2) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        words[0] = v.x;
+        words[1] = v.y;
+      } else {
 #pragma unroll
-    for (int s = 0; s < WPL; ++s) words[s] = vrow[min(w0 + s, p.KW - 1)];
+        for (int q = 0; q < WPL / 4; ++q) {
+          const uint4 v = *reinterpret_cast<const uint4*>(src + 4 * q);
+          words[4 * q] = v.x;
+          words[4 * q + 1] = v.y;
+          words[4 * q + 2] = v.z;
+          words[4 * q + 3] = v.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < WPL; ++s) words[s] = vrow[min(w0 + s, p.KW - 1)];
+    }
   }
   const float lv = lvec[min(r, R - 1)];
   const float lr = r < R ? lv : 0.f;
@@ -652,6 +673,62 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
     }
   }
 }
+
+// Sign words of one branch for a wave's steps [s0, s0 + n) of it.  Full
+// groups of 4 steps take one 16-byte load per lane: lane grp g takes the 4
+// words of step s0 + 4t + g and uses word u in MFMA iteration u of group t,
+// so the 4 lanes of a row read 64 contiguous bytes.  The n % 4 remaining
+// steps take one word per lane, word 4 * step + g.  Every lane issues
+// S / 4 + 3 loads whatever n is (clamped addresses), so that waits on earlier
+// loads stay exact.  A 16-byte load may run past its row into the next one
+// (those words meet ranks past R, whose t is zero); at the end of the matrix
+// (N * RW >= 4 words) the load start is clamped and sh records by how many
+// words the lane's words sit further on.
+template <int S>
+struct SignWords {
+  uint32_t grp[S / 4][4];
+  int sh[S / 4];
+  uint32_t rem[3];
+
+  __device__ __forceinline__ void load(const uint32_t* __restrict__ U, int row, int RW, int N, int steps_b, int s0,
+                                       int n, int g) {
+    const int G = n >> 2;
+    const int64_t rb = int64_t(row) * RW;
+    const int64_t last = int64_t(N) * RW - 4;
+#pragma unroll
+    for (int t = 0; t < S / 4; ++t) {
+      const int st = min(s0 + 4 * t + g, steps_b - 1);
+      const int64_t gi = rb + 4 * st;
+      const int64_t gl = gi < last ? gi : last;
+      uint4 v;
+      __builtin_memcpy(&v, U + gl, 16);
+      grp[t][0] = v.x;
+      grp[t][1] = v.y;
+      grp[t][2] = v.z;
+      grp[t][3] = v.w;
+      sh[t] = int(gi - gl);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int st = min(s0 + 4 * G + i, steps_b - 1);
+      rem[i] = U[rb + min(4 * st + g, RW - 1)];
+    }
+  }
+
+  // the 4 words of group t in step order (after an end-of-matrix shift)
+  __device__ __forceinline__ void group(int t, uint32_t (&w)[4]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = grp[t][e];
+    if (__builtin_amdgcn_ballot_w64(sh[t] != 0)) {
+      const int k = sh[t];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t a1 = grp[t][min(e + 1, 3)], a2 = grp[t][min(e + 2, 3)], a3 = grp[t][3];
+        w[e] = k == 0 ? w[e] : k == 1 ? a1 : k == 2 ? a2 : a3;
+      }
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b) [+ residual] per
@@ -758,19 +835,11 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   Raw8<float> v[L::MB][L::MR];
   load_chunk(min(tid, nch - 1), v);
 
-  // (2) sign words of the wave's steps: pre0[i] of branch 0 step q0 + i,
-  // pre1[i] of branch 1 step c1 + i
-  uint32_t pre0[S], pre1[S];
-  {
-    const int rw0 = P.RW[0], rw1 = two ? P.RW[1] : P.RW[0];
-    const uint32_t* __restrict__ r0 = P.U[0] + size_t(nc) * rw0;
-    const uint32_t* __restrict__ r1 = two ? P.U[1] + size_t(nc) * rw1 : r0;
-#pragma unroll
-    for (int i = 0; i < S; ++i) {
-      pre0[i] = r0[min(4 * (q0 + i) + grp, rw0 - 1)];
-      pre1[i] = r1[min(4 * (c1 + i) + grp, rw1 - 1)];
-    }
-  }
+  // (2) sign words of the wave's steps of each branch
+  SignWords<S> sw0, sw1;
+  sw0.load(P.U[0], nc, P.RW[0], P.N, steps0, q0, n0, grp);
+  if (two) sw1.load(P.U[1], nc, P.RW[1], P.N, P.RWp[1] / 4, c1, n1, grp);
+  else sw1.load(P.U[0], nc, P.RW[0], P.N, steps0, 0, 0, grp);  // same count of loads, never used
   // (3) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
   const float h0v = P.h[0][nc];
   const float h1v = P.h[two ? 1 : 0][nc];
@@ -805,34 +874,37 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
     acc0[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc1[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  auto run = [&](const SignWords<S>& sw, const u32x4* __restrict__ tb, int nchb, int s0, int n,
+                 f32x4 (&acc)[L::MB]) {
+    const int G = n >> 2, r = n & 3;
+    auto mfma4 = [&](uint32_t word, int w) {
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    if (i >= n0) continue;
-    const int w = 4 * (q0 + i) + grp;
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 bop = signs_to_bf16x8(word, j, kmask, kone);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bf16x8 bop = signs_to_bf16x8(pre0[i], j, kmask, kone);
-#pragma unroll
-      for (int mb = 0; mb < L::MB; ++mb) {
-        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb0[(size_t(mb) * nch0 + 4 * w + j) * L::ROWS + lrow]);
-        acc0[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc0[mb], 0, 0, 0);
+        for (int mb = 0; mb < L::MB; ++mb) {
+          const bf16x8 aop = __builtin_bit_cast(bf16x8, tb[(size_t(mb) * nchb + 4 * w + j) * L::ROWS + lrow]);
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc[mb], 0, 0, 0);
+        }
       }
+    };
+#pragma unroll
+    for (int t = 0; t < S / 4; ++t) {
+      if (t >= G) continue;
+      uint32_t w4[4];
+      sw.group(t, w4);
+      const int stp = s0 + 4 * t + grp;  // this lane's step of the group
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mfma4(w4[u], 4 * stp + u);
     }
-  }
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    if (i >= n1) continue;
-    const int w = 4 * (c1 + i) + grp;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bf16x8 bop = signs_to_bf16x8(pre1[i], j, kmask, kone);
-#pragma unroll
-      for (int mb = 0; mb < L::MB; ++mb) {
-        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb1[(size_t(mb) * nch1 + 4 * w + j) * L::ROWS + lrow]);
-        acc1[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc1[mb], 0, 0, 0);
-      }
+    for (int i = 0; i < 3; ++i) {
+      if (i >= r) continue;
+      mfma4(sw.rem[i], 4 * (s0 + 4 * G + i) + grp);
     }
-  }
+  };
+  run(sw0, tb0, nch0, q0, n0, acc0);
+  if (two) run(sw1, tb1, nch1, c1, n1, acc1);
   // h-weighted branch sums; C rows 4*grp + i (grp 0,1 hi, 2,3 lo of the same m)
   const float h1 = two ? h1v : 0.f;
   float out[L::MB][4];
@@ -1630,7 +1702,7 @@ struct ExpandChoice {
   int waves = 0, splits = 0, ws = 0;  // waves 0: no shape fits
 };
 
-// Expand launch shape: waves per block (4, 8 or 16) and waves per 16-row tile
+// Expand launch shape: waves per block (4 or 8) and waves per 16-row tile
 // (splits), by an estimate of the kernel's critical path in rank steps of one
 // wave: every pass of the t staging (a round trip to L2) weighs 8 steps and
 // repeats for each round of blocks the CUs cannot hold at once (blocks per
@@ -1642,15 +1714,14 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64
   ExpandChoice best;
   int64_t best_key[2] = {INT64_MAX, INT64_MAX};
   const int64_t mb = (mt + 7) / 8;
-  for (int waves : {4, 8, 16}) {
-    if (waves == 16 && mt > 8) continue;  // the staging registers of two m-blocks need more than 128 VGPRs
+  for (int waves : {4, 8}) {
     const int threads = waves * kWave;
     const size_t lds = lds2 + expand_static_lds(waves, mt);
     if (lds > size_t(kMaxBlockLds)) continue;
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(int64_t(kLdsPerCU) / int64_t(lds), 2048 / threads));
     for (int splits = 1; splits <= waves; splits *= 2) {
       const int64_t ws = ceil_div(steps, splits);
-      if (ws > kMaxWaveSteps || (waves == 16 && ws > 16)) continue;  // 16 waves: 128 VGPRs hold 16 steps' words
+      if (ws > kMaxWaveSteps) continue;
       const int tiles = waves / splits;
       int64_t blocks = 0;
       for (int q = 0; q < np; ++q) blocks += ceil_div(pd[q].N, 16 * tiles);
@@ -1673,10 +1744,12 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   int64_t nrb = 0, steps_max = 0, chunks_max = 0;
   size_t lds2 = 0;
   pl.mt = mtile(M);
+  bool small_u = false;  // a U matrix of fewer than 4 words: no 16-byte sign loads
   for (int q = 0; q < np; ++q) {
     int64_t rwp_sum = 0;
     for (int b = 0; b < pd[q].nb; ++b) {
       const int64_t R = pd[q].br[b].rank;
+      small_u = small_u || pd[q].N * ceil_div(R, 32) < 4;
       rwp_sum += ceil_div(ceil_div(R, 32), 4) * 4;
       nrb += ceil_div(R, kRowBlock);
     }
@@ -1687,7 +1760,7 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   }
   pl.nrb = int(nrb);
   const ExpandChoice ex = expand_shape(pd, np, pl.mt, lds2, chunks_max, steps_max);
-  pl.mfma = M >= 1 && M <= kMaxMfmaM && ex.waves > 0;
+  pl.mfma = M >= 1 && M <= kMaxMfmaM && ex.waves > 0 && !small_u;
   if (pl.mfma) {
     // enough blocks to cover the CUs, short per-wave chains
     pl.wpl = 2;
@@ -1739,9 +1812,6 @@ void launch_expand_mfma(const MfmaParams& p, int grid, size_t lds, hipStream_t s
 
 template <typename YT, int MT, int S>
 void dispatch_expand_waves(const MfmaParams& p, int waves, int grid, size_t lds, hipStream_t s) {
-  if constexpr (MT <= 8 && S <= 16) {
-    if (waves == 16) return launch_expand_mfma<YT, MT, S, 16>(p, grid, lds, s);
-  }
   if (waves == 8) launch_expand_mfma<YT, MT, S, 8>(p, grid, lds, s);
   else launch_expand_mfma<YT, MT, S, 4>(p, grid, lds, s);
 }
@@ -1782,6 +1852,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.nw = in.nw;
   p.eps = in.eps;
   bool xvec = (K % 8) == 0 && aligned16(x) && (!in.x1 || aligned16(in.x1)) && (!in.nw || aligned16(in.nw));
+  bool wvec = true;
   int rb = 0, tbase = 0, si = 0, tile = 0;
   for (int q = 0; q < np; ++q) {
     ExpProj& P = p.proj[q];
@@ -1812,6 +1883,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
       P.tbase[b] = tbase;
       rb += int(ceil_div(B.rank, kRowBlock));
       tbase += int(M) * S.RP;
+      wvec = wvec && (reinterpret_cast<uintptr_t>(B.v_sign) % 16) == 0;
       xvec = xvec && (reinterpret_cast<uintptr_t>(B.v2) % 16) == 0;
     }
   }
@@ -1819,6 +1891,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.tsize = tbase;
   p.nkc = pl.nkc;
   p.x = x;
+  p.wvec = wvec && p.KW % std::max(pl.wpl, 4) == 0 ? 1 : 0;
   p.xvec = xvec ? 1 : 0;
   char* ws = static_cast<char*>(workspace);
   p.sync = reinterpret_cast<uint32_t*>(ws);
