@@ -41,7 +41,10 @@ HBM_PEAK_GBS = 8000.0
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a 256 MiB device copy reads);
 # commands and figures in profiles/littlebit_decode_calls.md.  Measured for the
 # current kernels; a kind without a measurement reports null.
-MEASURED_TRAFFIC = {"down": 1_400_300}
+# HBM bytes per call (latent + expand kernels) from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE per dispatch, calibrated on a 256 MiB device copy (FETCH_SIZE
+# reads 0.5x the bytes moved, WRITE_SIZE 1.0x); `--only <kind>` graphs.
+MEASURED_TRAFFIC = {"qkv": 1_411_789, "o": 699_084, "gate/up": 1_983_898, "down": 1_514_188}
 MALL_BYTES = 256 << 20
 
 
