@@ -386,8 +386,9 @@ __device__ __forceinline__ void load_input8(const MfmaParams& p, const float* __
   }
 }
 
-// Blocks are dispatched to the 8 XCDs of MI355X round-robin (block b runs on
-// XCD b % 8, confirmed on the device).  This maps block b to a logical index
+// Blocks are dispatched to the 8 XCDs of MI355X round-robin: blocks b and
+// b + 8 run on the same XCD (measured with HW_REG_XCC_ID; which XCD block 0
+// lands on varies between launches).  This maps block b to a logical index
 // so that each XCD gets one contiguous range of logical blocks: neighbouring
 // k-chunks of a row-block, which share 128-byte lines of the sign rows, then
 // meet in one L2 instead of fetching the line from HBM once per XCD.  Any
