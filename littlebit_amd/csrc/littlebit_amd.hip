@@ -143,11 +143,14 @@ struct Raw8<uint16_t> {
 // ---------------------------------------------------------------------------
 // MFMA path parameters
 // ---------------------------------------------------------------------------
-constexpr int kMaxWaveSteps = 24;  // sign-word steps per branch per expand wave
+constexpr int kMaxWaveSteps = 32;  // rank steps (both branches) per expand wave
 constexpr int kMaxProj = 4;        // projections sharing one input in a group call
 constexpr int kMaxSeg = 2 * kMaxProj;
 // floats per latent half: M <= 16 rows of the padded ranks of every branch
 constexpr int kTHalf = kMaxMfmaM * (kMaxRankTotal + kMaxSeg * 128);
+// t of a call pads each branch's rank by less than 128, so the sums of
+// squares after it always fit
+static_assert(kMaxMfmaM * (kMaxRankTotal + kMaxSeg * 127) + kMaxMfmaM <= kTHalf, "latent half too small");
 
 // Stage-1 operands of one branch ("segment") of a group call.
 struct LatSeg {
@@ -187,11 +190,13 @@ struct MfmaParams {
   int xvec;     // x (x1, rms weight) and every g allow 16-byte loads (aligned, K % 8 == 0)
   int wvec;     // V rows allow WPL-word vector loads (16-byte aligned rows, KW % max(WPL, 4) == 0)
   int xmode;    // LBK_INPUT_*: x as is, RMSNorm(x) * w, or SiLU(x) * x1
+  int late_rs;  // RMSNorm input staged without 1/rms: expand_mfma_kernel scales t
   const void* x;
   const void* x1;       // second input of LBK_INPUT_SILU_MUL
   const float* nw;      // RMSNorm weight [K]
   float eps;            // RMSNorm epsilon
-  float* t2;       // two halves of kTHalf floats; per segment [M][RP] latent, l-scaled
+  float* t2;       // two halves of kTHalf floats; per segment [M][RP] latent, l-scaled,
+                   // then kMaxMfmaM floats: per row the sum of x^2 (RMSNorm input)
   uint32_t* sync;  // [0] P: half the next latent kernel accumulates into
                    // [1] Q: half the last latent kernel accumulated into
                    // [2 + h] floats of half h that may be non-zero
@@ -201,7 +206,8 @@ struct MfmaParams {
 // blocks is needed; kernel boundaries order the rest):
 //   latent_mfma_kernel: h = P; accumulate into half h (which is zero);
 //     clear the first S[1-h] floats of half 1-h (making it all zero);
-//     block 0 writes Q = h and S[h] = tsize.
+//     block 0 writes Q = h and S[h] = tsize + kMaxMfmaM (t, then the rows'
+//     sums of squares of an RMSNorm input, added by the first row-block).
 //   expand_mfma_kernel: reads t from half Q; block 0 writes P = 1 - Q.
 // Calls of any shape may follow each other on one workspace; graph replay
 // works because the state lives in device memory, not in kernel arguments.
@@ -313,41 +319,6 @@ __device__ __forceinline__ void rms_scales(const XT* __restrict__ x, int M, int 
   rms_finish<MT, BLOCK>(part, K, eps, rs, scratch, tid);
 }
 
-// Per-thread partial sums of x[m, k]^2 for m < MT (rows past M read row
-// M - 1; their scales are never used) over this thread's 8-element groups
-// k = 8 * (tid + BLOCK * j); rows 16-byte aligned, K % 8 == 0.  Rows go in
-// groups of up to 4, two 8-element groups of each in flight at clamped
-// addresses, so a row group costs one round trip when K <= 16 * BLOCK.
-template <typename XT, int MT, int BLOCK>
-__device__ __forceinline__ void sumsq_vec(const XT* __restrict__ x, int M, int K, float (&part)[MT], int tid) {
-  constexpr int RG = MT < 4 ? MT : 4;
-  const int K8 = K / 8;
-#pragma unroll
-  for (int m = 0; m < MT; ++m) part[m] = 0.f;
-  for (int g0 = 0; g0 < K8; g0 += 2 * BLOCK) {
-#pragma unroll
-    for (int m0 = 0; m0 < MT; m0 += RG) {
-      Raw8<XT> r[RG][2];
-#pragma unroll
-      for (int i = 0; i < RG; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          r[i][j].load(x + size_t(min(m0 + i, M - 1)) * K + 8 * min(g0 + tid + BLOCK * j, K8 - 1));
-#pragma unroll
-      for (int i = 0; i < RG; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          float a[8];
-          r[i][j].get(a);
-          float s = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s += a[e] * a[e];
-          part[m0 + i] += g0 + tid + BLOCK * j < K8 ? s : 0.f;
-        }
-    }
-  }
-}
-
 // 8 effective inputs (m, kb .. kb+7) times g, zeros past K.
 template <typename XT>
 __device__ __forceinline__ void load_input8(const MfmaParams& p, const float* __restrict__ g, int m, int kb,
@@ -424,97 +395,118 @@ __device__ __forceinline__ void build_compact(u32x4* lds, int nch, int M, int ti
   }
 }
 
-// Effective input (times g) of the 8 k from kb of every stored row of the
-// compact A operand, input mode MODE, vector path (x, x1, g and the RMSNorm
-// weight 16-byte aligned, K % 8 == 0: a chunk lies wholly inside K or wholly
-// past it).  load() issues every load at clamped addresses; get() computes
-// what load_input8 computes, in the same order, zero past K.
-template <typename XT, int MT, int MODE>
-struct InputChunk {
-  using L = Compact<MT>;
+// RPT rows m0 .. m0 + RPT - 1 of the effective input times g for one chunk of
+// 8 k from kb, vector path (x, x1, g and the RMSNorm weight 16-byte aligned,
+// K % 8 == 0: a chunk lies wholly inside K or wholly past it).  load() issues
+// every load at clamped addresses (rows past M read row M - 1).  get() gives
+// row i times g, zero past K -- for RMSNorm x * w * g without the row's 1/rms,
+// which multiplies t instead (the expand kernel applies it); sq() gives the
+// row's sum of x^2 over the chunk.
+template <typename XT, int RPT, int MODE>
+struct RowChunk {
   static constexpr bool kSilu = MODE == LBK_INPUT_SILU_MUL;
-  Raw8<XT> xr[L::MB][L::MR];
-  Raw8<XT> ur[kSilu ? L::MB : 1][kSilu ? L::MR : 1];
+  Raw8<XT> xr[RPT];
+  Raw8<XT> ur[kSilu ? RPT : 1];
   Raw8<float> gr, wr;
   bool valid;
 
-  __device__ __forceinline__ void load(const MfmaParams& p, const float* __restrict__ g, int kb) {
+  __device__ __forceinline__ void load(const MfmaParams& p, const float* __restrict__ g, int kb, int m0) {
     valid = kb < p.K;
     const int kl = valid ? kb : 0;
     const XT* __restrict__ x = static_cast<const XT*>(p.x);
     gr.load(g + kl);
     if constexpr (MODE == LBK_INPUT_RMSNORM) wr.load(p.nw + kl);
 #pragma unroll
-    for (int mb = 0; mb < L::MB; ++mb)
-#pragma unroll
-      for (int ml = 0; ml < L::MR; ++ml) {
-        const size_t at = size_t(min(mb * 8 + ml, p.M - 1)) * p.K + kl;
-        xr[mb][ml].load(x + at);
-        if constexpr (kSilu) ur[mb][ml].load(static_cast<const XT*>(p.x1) + at);
-      }
+    for (int i = 0; i < RPT; ++i) {
+      const size_t at = size_t(min(m0 + i, p.M - 1)) * p.K + kl;
+      xr[i].load(x + at);
+      if constexpr (kSilu) ur[i].load(static_cast<const XT*>(p.x1) + at);
+    }
   }
 
-  __device__ __forceinline__ void get(int mb, int ml, float rsm, float (&a)[8]) const {
+  __device__ __forceinline__ void get(int i, float (&a)[8]) const {
     float gv[8];
     gr.get(gv);
-    xr[mb][ml].get(a);
+    xr[i].get(a);
     if constexpr (MODE == LBK_INPUT_RMSNORM) {
       float wv[8];
       wr.get(wv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) gv[i] *= wv[i] * rsm;
+      for (int e = 0; e < 8; ++e) gv[e] *= wv[e];
     } else if constexpr (kSilu) {
       float uv[8];
-      ur[mb][ml].get(uv);
+      ur[i].get(uv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = silu_f(a[i]) * uv[i];
+      for (int e = 0; e < 8; ++e) a[e] = silu_f(a[e]) * uv[e];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = valid ? a[i] * gv[i] : 0.f;
+    for (int e = 0; e < 8; ++e) a[e] = valid ? a[e] * gv[e] : 0.f;
+  }
+
+  __device__ __forceinline__ float sq(int i) const {
+    float a[8];
+    xr[i].get(a);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += a[e] * a[e];
+    return valid ? s : 0.f;
   }
 };
 
 // The latent kernel's compact A operand of one k-chunk (NCH chunks of 8 k
-// from k0), vector path: thread tid < NCH owns chunk tid.  The chunk's loads
-// and, for RMSNorm, the loads of every row's sums of squares are all issued
-// before the first wait.  Ends with this thread's LDS writes, no barrier.
+// from k0), vector path.  The NCH * MT (chunk, row) pairs are spread over the
+// block: thread tid takes chunk tid % NCH and RPT rows from RPT * (tid / NCH),
+// so consecutive threads read consecutive chunks of a row and no thread holds
+// more than RPT rows; waves with no pair skip as a whole.  With ssq (RMSNorm,
+// one row-block per k-chunk) the chunk's sums of x^2 of every row m < M are
+// added into ssq_out[m].  Ends with this thread's LDS writes, no barrier.
 template <typename XT, int MT, int NCH, int MODE>
-__device__ __forceinline__ void stage_latent_vec(const MfmaParams& p, const float* __restrict__ g, int k0,
-                                                 u32x4* lds, int tid) {
+__device__ __forceinline__ void stage_latent_rows(const MfmaParams& p, const float* __restrict__ g, int k0,
+                                                  u32x4* lds, int tid, bool ssq, float* ssq_out) {
   using L = Compact<MT>;
-  static_assert(NCH <= kBlock, "one chunk per thread");
-  const int c = min(tid, NCH - 1);
-  InputChunk<XT, MT, MODE> in;
-  in.load(p, g, k0 + 8 * c);
-  float rsv[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
+  constexpr int RG = MT < kBlock / NCH ? MT : kBlock / NCH;  // row groups (threads per chunk)
+  constexpr int RPT = MT / RG;                                // rows per thread
+  constexpr int PAIRS = NCH * RG;                             // active threads
+  static_assert(RG * RPT == MT && PAIRS <= kBlock, "row groups");
+  if (tid - (tid & 63) >= PAIRS) return;  // the whole wave is idle
+  const bool active = tid < PAIRS;
+  const int c = tid % NCH;
+  const int rg = active ? tid / NCH : 0;
+  const int m0 = rg * RPT;
+  RowChunk<XT, RPT, MODE> in;
+  in.load(p, g, k0 + 8 * c, m0);
   if constexpr (MODE == LBK_INPUT_RMSNORM) {
-    __shared__ float rs[MT];
-    __shared__ float scratch[kBlock / 64 * MT];
-    float part[MT];
-    sumsq_vec<XT, MT, kBlock>(static_cast<const XT*>(p.x), p.M, p.K, part, tid);
-    rms_finish<MT, kBlock>(part, p.K, p.eps, rs, scratch, tid);
+    if (ssq) {
+      // lanes of one row group are contiguous: reduce over them, then one
+      // atomic per row from the group's first lane
+      constexpr int SPAN = NCH < 64 ? NCH : 64;
 #pragma unroll
-    for (int m = 0; m < MT; ++m) rsv[m] = rs[m];
-  }
-  if (tid < NCH) {
+      for (int i = 0; i < RPT; ++i) {
+        float v = active ? in.sq(i) : 0.f;
 #pragma unroll
-    for (int mb = 0; mb < L::MB; ++mb) {
-      u32x4* base = lds + (size_t(mb) * NCH + c) * L::ROWS;
-#pragma unroll
-      for (int ml = 0; ml < L::MR; ++ml) {
-        u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
-        if (mb * 8 + ml < p.M) {
-          float a[8];
-          in.get(mb, ml, rsv[mb * 8 + ml], a);
-          split8(a, hi, lo);
-        }
-        base[ml] = hi;
-        base[L::MR + ml] = lo;
+        for (int o = SPAN / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+        if (active && (tid % SPAN) == 0 && m0 + i < p.M) unsafeAtomicAdd(ssq_out + m0 + i, v);
       }
-      base[2 * L::MR] = u32x4{0u, 0u, 0u, 0u};
     }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int m = m0 + i;
+    const int mb = m / 8, ml = m % 8;
+    u32x4* base = lds + (size_t(mb) * NCH + c) * L::ROWS;
+    u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+    if (m < p.M) {
+      float a[8];
+      in.get(i, a);
+      split8(a, hi, lo);
+    }
+    base[ml] = hi;
+    base[L::MR + ml] = lo;
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb) lds[(size_t(mb) * NCH + c) * L::ROWS + 2 * L::MR] = u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -603,9 +595,16 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 
   // ---- A operand: hi/lo bf16 of g[k] * input[m, k] for this k-chunk ----
   if (p.xvec) {
-    if (p.xmode == LBK_INPUT_RMSNORM) stage_latent_vec<XT, MT, NCH, LBK_INPUT_RMSNORM>(p, g, k0, lds_a, tid);
-    else if (p.xmode == LBK_INPUT_SILU_MUL) stage_latent_vec<XT, MT, NCH, LBK_INPUT_SILU_MUL>(p, g, k0, lds_a, tid);
-    else stage_latent_vec<XT, MT, NCH, LBK_INPUT_PLAIN>(p, g, k0, lds_a, tid);
+    // RMSNorm: t is accumulated without the rows' 1/rms; the blocks of the
+    // first row-block add their chunk's sums of squares next to t, and the
+    // expand kernel scales t by 1/rms when it stages it
+    float* ssq_out = p.t2 + size_t(h) * kTHalf + p.tsize;
+    if (p.xmode == LBK_INPUT_RMSNORM)
+      stage_latent_rows<XT, MT, NCH, LBK_INPUT_RMSNORM>(p, g, k0, lds_a, tid, rbk == 0, ssq_out);
+    else if (p.xmode == LBK_INPUT_SILU_MUL)
+      stage_latent_rows<XT, MT, NCH, LBK_INPUT_SILU_MUL>(p, g, k0, lds_a, tid, false, ssq_out);
+    else
+      stage_latent_rows<XT, MT, NCH, LBK_INPUT_PLAIN>(p, g, k0, lds_a, tid, false, ssq_out);
   } else {
     __shared__ float rs[MT];
     if (p.xmode == LBK_INPUT_RMSNORM) {
@@ -670,36 +669,52 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
     for (int i = lo + tid; i < hi; i += kBlock) other[i] = 0.f;
     if (blockIdx.x == 0 && tid == 0) {
       __hip_atomic_store(p.sync + 1, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(p.sync + 2 + h, uint32_t(p.tsize), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.sync + 2 + h, uint32_t(p.tsize + kMaxMfmaM), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
-// Sign words of one branch for a wave's steps [s0, s0 + n) of it.  Full
-// groups of 4 steps take one 16-byte load per lane: lane grp g takes the 4
-// words of step s0 + 4t + g and uses word u in MFMA iteration u of group t,
-// so the 4 lanes of a row read 64 contiguous bytes.  The n % 4 remaining
-// steps take one word per lane, word 4 * step + g.  Every lane issues
-// S / 4 + 3 loads whatever n is (clamped addresses), so that waits on earlier
-// loads stay exact.  A 16-byte load may run past its row into the next one
-// (those words meet ranks past R, whose t is zero); at the end of the matrix
-// (N * RW >= 4 words) the load start is clamped and sh records by how many
-// words the lane's words sit further on.
+// A projection's branches as the expand kernel's waves walk them: the rank
+// steps (4 sign words of a U row) of branch 0, padded to a multiple of 4
+// when branch 1 follows (P0 steps), then those of branch 1, so that no group
+// of 4 consecutive steps from a multiple of 4 spans both branches.  With one
+// branch, "branch 1" repeats branch 0 from P0 = its step count (no group
+// reaches it).  Fields are wave-uniform.
+struct StepSeq {
+  const uint32_t* U[2];
+  int RW[2];     // words per U row
+  int steps[2];  // RWp / 4
+  int P0;
+  int N;
+};
+
+// Sign words of a wave's steps [q0, q1) of a StepSeq, q0 a multiple of 4.
+// Full groups take one 16-byte load per lane: lane grp g takes the 4 words of
+// step q0 + 4t + g and uses word u in MFMA iteration u of group t, so the 4
+// lanes of a row read 64 contiguous bytes.  The (q1 - q0) % 4 steps left at
+// the end of the sequence take one word per lane, word 4 * step + g.  Every
+// lane issues S / 4 + 3 loads whatever the range is (clamped addresses), so
+// that waits on earlier loads stay exact.  A 16-byte load may run past its row
+// into the next one (those words meet ranks past R, whose t is zero); at the
+// end of the matrix (N * RW >= 4 words) the load start is clamped and sh
+// records by how many words the lane's words sit further on.
 template <int S>
 struct SignWords {
   uint32_t grp[S / 4][4];
   int sh[S / 4];
   uint32_t rem[3];
 
-  __device__ __forceinline__ void load(const uint32_t* __restrict__ U, int row, int RW, int N, int steps_b, int s0,
-                                       int n, int g) {
-    const int G = n >> 2;
-    const int64_t rb = int64_t(row) * RW;
-    const int64_t last = int64_t(N) * RW - 4;
+  __device__ __forceinline__ void load(const StepSeq& b, int row, int q0, int q1, int g) {
+    const int G = (q1 - q0) >> 2;
 #pragma unroll
     for (int t = 0; t < S / 4; ++t) {
-      const int st = min(s0 + 4 * t + g, steps_b - 1);
-      const int64_t gi = rb + 4 * st;
+      const bool b1 = q0 + 4 * t >= b.P0;  // the group's branch (uniform)
+      const uint32_t* __restrict__ U = b1 ? b.U[1] : b.U[0];
+      const int RW = b1 ? b.RW[1] : b.RW[0];
+      const int nst = b1 ? b.steps[1] : b.steps[0];
+      const int st = min((b1 ? q0 + 4 * t - b.P0 : q0 + 4 * t) + g, nst - 1);
+      const int64_t gi = int64_t(row) * RW + 4 * st;
+      const int64_t last = int64_t(b.N) * RW - 4;
       const int64_t gl = gi < last ? gi : last;
       uint4 v;
       __builtin_memcpy(&v, U + gl, 16);
@@ -711,8 +726,12 @@ struct SignWords {
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      const int st = min(s0 + 4 * G + i, steps_b - 1);
-      rem[i] = U[rb + min(4 * st + g, RW - 1)];
+      const int q = q0 + 4 * G + i;
+      const bool b1 = q >= b.P0;
+      const uint32_t* __restrict__ U = b1 ? b.U[1] : b.U[0];
+      const int RW = b1 ? b.RW[1] : b.RW[0];
+      const int st = min(b1 ? q - b.P0 : q, (b1 ? b.steps[1] : b.steps[0]) - 1);
+      rem[i] = U[int64_t(row) * RW + min(4 * st + g, RW - 1)];
     }
   }
 
@@ -735,9 +754,9 @@ struct SignWords {
 // Stage 2 (MFMA): y = bias + sum_b h_b * (U_b_sign . t_b) [+ residual] per
 // projection.  block = WAVES waves over 16 * tiles output rows of one
 // projection, tiles = WAVES / splits: wave w owns row tile w % tiles and part
-// w / tiles of the rank steps (4 sign words of a row) of both branches taken
-// in sequence; the splits parts of a tile meet in LDS.  Every block stages all
-// of its projection's t.  The host picks WAVES and splits.
+// w / tiles of the projection's StepSeq (with two branches a multiple of 4
+// steps per part); the splits parts of a tile meet in LDS.  Every block stages all of its
+// projection's t.  The host picks WAVES and splits.
 // grid.x = sum over projections of ceil(N / (16 * tiles))
 // LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
 //
@@ -776,16 +795,21 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   // block 0 writes the state here, and only sync[0]
   const uint32_t hq = p.sync[1] & 1u;
 
-  // this wave's steps [q0, q1) of the branches in sequence: n0 steps of
-  // branch 0 from step q0, then n1 steps of branch 1 from its step c1
-  const int steps0 = P.RWp[0] / 4;
-  const int steps = steps0 + (two ? P.RWp[1] / 4 : 0);
-  const int per = (steps + splits - 1) / splits;
-  const int q0 = min(part * per, steps);
-  const int q1 = min(q0 + per, steps);
-  const int n0 = max(min(q1, steps0) - q0, 0);
-  const int c1 = max(q0, steps0) - steps0;
-  const int n1 = max(q1 - max(q0, steps0), 0);
+  // the projection's steps in sequence and this wave's part [q0, q1) of them
+  StepSeq sq;
+  sq.U[0] = P.U[0];
+  sq.U[1] = P.U[two ? 1 : 0];
+  sq.RW[0] = __builtin_amdgcn_readfirstlane(P.RW[0]);
+  sq.RW[1] = __builtin_amdgcn_readfirstlane(P.RW[two ? 1 : 0]);
+  sq.steps[0] = __builtin_amdgcn_readfirstlane(P.RWp[0] / 4);
+  sq.steps[1] = __builtin_amdgcn_readfirstlane(P.RWp[two ? 1 : 0] / 4);
+  sq.P0 = two ? (sq.steps[0] + 3) & ~3 : sq.steps[0];
+  sq.N = P.N;
+  const int nsteps = sq.P0 + (two ? sq.steps[1] : 0);
+  // parts of a two-branch sequence start at multiples of 4 (no group spans P0)
+  const int per = two ? 4 * ((nsteps + 4 * splits - 1) / (4 * splits)) : (nsteps + splits - 1) / splits;
+  const int q0 = min(part * per, nsteps);
+  const int q1 = min(q0 + per, nsteps);
 
   // (1) this thread's first staging chunk: chunk q of the chunks of both
   // branches in sequence, every stored row
@@ -811,6 +835,11 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
 #pragma unroll
       for (int ml = 0; ml < L::MR; ++ml) v[mb][ml].load(src + size_t(min(mb * 8 + ml, M - 1)) * rp);
   };
+  // 1/rms of each row when t was accumulated without it (RMSNorm input):
+  // the rows' sums of squares follow t in the same half, 16-byte aligned (t
+  // is a multiple of 128 floats), read with 16-byte loads
+  Raw8<float> ssq[(MT + 7) / 8];
+  float rsv[MT];  // set before the staging: 1/rms, or 1
   auto put_chunk = [&](int q, const Raw8<float> (&v)[L::MB][L::MR]) {
     const bool b1 = q >= nch0;
     const int c = b1 ? q - nch0 : q;
@@ -825,6 +854,8 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
         if (mb * 8 + ml < M) {
           float a[8];
           v[mb][ml].get(a);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] *= rsv[mb * 8 + ml];
           split8(a, hi, lo);
         }
         base[ml] = hi;
@@ -834,13 +865,13 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
     }
   };
   Raw8<float> v[L::MB][L::MR];
-  load_chunk(min(tid, nch - 1), v);
+  if (tid - lane < nch) load_chunk(min(tid, nch - 1), v);  // waves with no chunk skip
+#pragma unroll
+  for (int i = 0; i < (MT + 7) / 8; ++i) ssq[i].load(ta + p.tsize + 8 * i);
 
-  // (2) sign words of the wave's steps of each branch
-  SignWords<S> sw0, sw1;
-  sw0.load(P.U[0], nc, P.RW[0], P.N, steps0, q0, n0, grp);
-  if (two) sw1.load(P.U[1], nc, P.RW[1], P.N, P.RWp[1] / 4, c1, n1, grp);
-  else sw1.load(P.U[0], nc, P.RW[0], P.N, steps0, 0, 0, grp);  // same count of loads, never used
+  // (2) sign words of the wave's steps
+  SignWords<S> sw;
+  sw.load(sq, nc, q0, q1, grp);
   // (3) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
   const float h0v = P.h[0][nc];
   const float h1v = P.h[two ? 1 : 0][nc];
@@ -858,6 +889,17 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
 
   // (4) staging: the first chunk (waits for its loads only), then any chunks
   // past the first THREADS
+  {
+    const bool late = p.late_rs != 0;
+    const float kf = float(p.K), eps = p.eps;
+#pragma unroll
+    for (int i = 0; i < (MT + 7) / 8; ++i) {
+      float a[8];
+      ssq[i].get(a);
+#pragma unroll
+      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = late ? 1.f / sqrtf(a[e] / kf + eps) : 1.f;
+    }
+  }
   if (tid < nch) put_chunk(tid, v);
   for (int q = tid + THREADS; q < nch; q += THREADS) {
     load_chunk(q, v);
@@ -865,47 +907,75 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   }
   __syncthreads();
 
-  // (5) MFMA over the wave's steps, branch 0 then branch 1
+  // (5) MFMA over the wave's steps, branch 0 then branch 1: acc holds the
+  // branch being walked; on entering branch 1 it moves to acc0
   uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
   asm volatile("" : "+v"(kmask), "+v"(kone));
   const int lrow = L::lane_row(col);
-  f32x4 acc0[L::MB], acc1[L::MB];
+  f32x4 acc[L::MB], acc0[L::MB];
 #pragma unroll
   for (int mb = 0; mb < L::MB; ++mb) {
+    acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc0[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc1[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  auto run = [&](const SignWords<S>& sw, const u32x4* __restrict__ tb, int nchb, int s0, int n,
-                 f32x4 (&acc)[L::MB]) {
-    const int G = n >> 2, r = n & 3;
-    auto mfma4 = [&](uint32_t word, int w) {
+  bool in1 = false;  // acc holds branch 1 (wave-uniform)
+  auto enter = [&](bool b1) {
+    if (b1 && !in1) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 bop = signs_to_bf16x8(word, j, kmask, kone);
-#pragma unroll
-        for (int mb = 0; mb < L::MB; ++mb) {
-          const bf16x8 aop = __builtin_bit_cast(bf16x8, tb[(size_t(mb) * nchb + 4 * w + j) * L::ROWS + lrow]);
-          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc[mb], 0, 0, 0);
-        }
+      for (int mb = 0; mb < L::MB; ++mb) {
+        acc0[mb] = acc[mb];
+        acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    };
+      in1 = true;
+    }
+  };
+  // 4 MFMAs over word w of the lane's step (chunks 4w .. 4w + 3 of the
+  // branch's t); km = ko = 0 gives a zero B operand
+  auto mfma4 = [&](uint32_t word, const u32x4* __restrict__ tb, int nchb, int w, uint32_t km, uint32_t ko) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 bop = signs_to_bf16x8(word, j, km, ko);
+#pragma unroll
+      for (int mb = 0; mb < L::MB; ++mb) {
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb[(size_t(mb) * nchb + 4 * w + j) * L::ROWS + lrow]);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc[mb], 0, 0, 0);
+      }
+    }
+  };
+  {
+    const int n = q1 - q0, G = n >> 2, r = n & 3;
 #pragma unroll
     for (int t = 0; t < S / 4; ++t) {
       if (t >= G) continue;
+      const bool b1 = q0 + 4 * t >= sq.P0;
+      enter(b1);
       uint32_t w4[4];
       sw.group(t, w4);
-      const int stp = s0 + 4 * t + grp;  // this lane's step of the group
+      // this lane's step of the group within its branch; steps in branch 0's
+      // padding get a zero B operand (and read chunk 0)
+      const int st = (b1 ? q0 + 4 * t - sq.P0 : q0 + 4 * t) + grp;
+      const bool valid = b1 || st < sq.steps[0];
+      const int sv = valid ? st : 0;
+      const uint32_t km = valid ? kmask : 0u, ko = valid ? kone : 0u;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) mfma4(w4[u], 4 * stp + u);
+      for (int u = 0; u < 4; ++u) mfma4(w4[u], b1 ? tb1 : tb0, b1 ? nch1 : nch0, 4 * sv + u, km, ko);
     }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       if (i >= r) continue;
-      mfma4(sw.rem[i], 4 * (s0 + 4 * G + i) + grp);
+      const int q = q0 + 4 * G + i;
+      const bool b1 = q >= sq.P0;
+      enter(b1);
+      mfma4(sw.rem[i], b1 ? tb1 : tb0, b1 ? nch1 : nch0, 4 * (b1 ? q - sq.P0 : q) + grp, kmask, kone);
     }
-  };
-  run(sw0, tb0, nch0, q0, n0, acc0);
-  if (two) run(sw1, tb1, nch1, c1, n1, acc1);
+  }
+  if (!in1) {
+#pragma unroll
+    for (int mb = 0; mb < L::MB; ++mb) {
+      acc0[mb] = acc[mb];
+      acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
   // h-weighted branch sums; C rows 4*grp + i (grp 0,1 hi, 2,3 lo of the same m)
   const float h1 = two ? h1v : 0.f;
   float out[L::MB][4];
@@ -914,7 +984,7 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       out[mb][i] = h0v * (acc0[mb][i] + __shfl_xor(acc0[mb][i], 32)) +
-                   h1 * (acc1[mb][i] + __shfl_xor(acc1[mb][i], 32));
+                   h1 * (acc[mb][i] + __shfl_xor(acc[mb][i], 32));
 
   // (6) the other parts of the tile add theirs through LDS
   if (splits > 1) {
@@ -1708,9 +1778,21 @@ struct ExpandChoice {
 // wave: every pass of the t staging (a round trip to L2) weighs 8 steps and
 // repeats for each round of blocks the CUs cannot hold at once (blocks per
 // CU bounded by LDS and by 2048 threads); the busiest SIMD then runs
-// ceil(blocks / 256) * waves / 4 waves of ceil(steps / splits) steps each.
+// ceil(blocks / 256) * waves / 4 waves of part_steps() steps each.
 // Ties go to fewer blocks (less staging traffic).
-ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64_t chunks, int64_t steps) {
+// Rank steps of projection q as expand_mfma_kernel walks them (branch 0's
+// padded to a multiple of 4 when branch 1 follows) and the steps of one of
+// `splits` parts.
+int64_t proj_steps(const ProjDesc& d) {
+  const int64_t st0 = ceil_div(ceil_div(d.br[0].rank, 32), 4);
+  return d.nb > 1 ? (st0 + 3) / 4 * 4 + ceil_div(ceil_div(d.br[1].rank, 32), 4) : st0;
+}
+int64_t part_steps(const ProjDesc& d, int splits) {
+  const int64_t n = proj_steps(d);
+  return d.nb > 1 ? 4 * ceil_div(n, 4 * splits) : ceil_div(n, splits);
+}
+
+ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64_t chunks) {
   constexpr int kCUs = 256;
   ExpandChoice best;
   int64_t best_key[2] = {INT64_MAX, INT64_MAX};
@@ -1721,7 +1803,8 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64
     if (lds > size_t(kMaxBlockLds)) continue;
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(int64_t(kLdsPerCU) / int64_t(lds), 2048 / threads));
     for (int splits = 1; splits <= waves; splits *= 2) {
-      const int64_t ws = ceil_div(steps, splits);
+      int64_t ws = 0;
+      for (int q = 0; q < np; ++q) ws = std::max(ws, part_steps(pd[q], splits));
       if (ws > kMaxWaveSteps) continue;
       const int tiles = waves / splits;
       int64_t blocks = 0;
@@ -1742,7 +1825,7 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64
 
 Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   Plan pl{};
-  int64_t nrb = 0, steps_max = 0, chunks_max = 0;
+  int64_t nrb = 0, chunks_max = 0;
   size_t lds2 = 0;
   pl.mt = mtile(M);
   bool small_u = false;  // a U matrix of fewer than 4 words: no 16-byte sign loads
@@ -1757,19 +1840,19 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     const size_t l2 = compact_rows(pl.mt, 4 * rwp_sum) * 16;
     if (4 * rwp_sum > chunks_max) chunks_max = 4 * rwp_sum;
     if (l2 > lds2) lds2 = l2;
-    if (rwp_sum / 4 > steps_max) steps_max = rwp_sum / 4;  // rank steps of the projection
   }
   pl.nrb = int(nrb);
-  const ExpandChoice ex = expand_shape(pd, np, pl.mt, lds2, chunks_max, steps_max);
+  const ExpandChoice ex = expand_shape(pd, np, pl.mt, lds2, chunks_max);
   pl.mfma = M >= 1 && M <= kMaxMfmaM && ex.waves > 0 && !small_u;
   if (pl.mfma) {
     // enough blocks to cover the CUs, short per-wave chains
+    // (MT * WPL <= 64 keeps the staging at <= 4 rows per thread)
     pl.wpl = 2;
     for (int w : {8, 4}) {
-      if (nrb * ceil_div(K, 128 * w) >= 256) { pl.wpl = w; break; }
+      if (pl.mt * w <= 64 && nrb * ceil_div(K, 128 * w) >= 256) { pl.wpl = w; break; }
     }
     pl.nkc = int(ceil_div(K, 128 * pl.wpl));
-    pl.wsteps = ex.ws <= 4 ? 4 : ex.ws <= 8 ? 8 : ex.ws <= 16 ? 16 : kMaxWaveSteps;
+    pl.wsteps = ex.ws <= 4 ? 4 : ex.ws <= 8 ? 8 : ex.ws <= 16 ? 16 : ex.ws <= 24 ? 24 : kMaxWaveSteps;
     pl.lds1 = compact_rows(pl.mt, 128 * pl.wpl / 8) * 16;
     pl.lds2 = lds2;
     pl.waves = ex.waves;
@@ -1823,6 +1906,7 @@ void dispatch_expand_s(const MfmaParams& p, const Plan& pl, int grid, hipStream_
     case 4: dispatch_expand_waves<YT, MT, 4>(p, pl.waves, grid, pl.lds2, s); break;
     case 8: dispatch_expand_waves<YT, MT, 8>(p, pl.waves, grid, pl.lds2, s); break;
     case 16: dispatch_expand_waves<YT, MT, 16>(p, pl.waves, grid, pl.lds2, s); break;
+    case 24: dispatch_expand_waves<YT, MT, 24>(p, pl.waves, grid, pl.lds2, s); break;
     default: dispatch_expand_waves<YT, MT, kMaxWaveSteps>(p, pl.waves, grid, pl.lds2, s); break;
   }
 }
@@ -1894,6 +1978,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.x = x;
   p.wvec = wvec && p.KW % std::max(pl.wpl, 4) == 0 ? 1 : 0;
   p.xvec = xvec ? 1 : 0;
+  p.late_rs = xvec && in.kind == LBK_INPUT_RMSNORM ? 1 : 0;
   char* ws = static_cast<char*>(workspace);
   p.sync = reinterpret_cast<uint32_t*>(ws);
   p.t2 = reinterpret_cast<float*>(ws + kTOffset);
