@@ -760,10 +760,11 @@ struct SignWords {
 // grid.x = sum over projections of ceil(N / (16 * tiles))
 // LDS: compact A operands of t, branch 0 then branch 1 (4*RWp chunks each)
 //
-// Every load the block needs -- the first staging chunk of each thread, the
-// sign words, h, bias and residual -- is issued before the first wait, at
-// clamped addresses so that no path skips a load: rows past N are never
-// stored, and sign words past a row meet ranks past R, whose t is zero.
+// Every load the block needs -- the sign words, h, bias and residual, then
+// each thread's first staging chunk (whose address needs the latent-buffer
+// half, read from memory) -- is issued before the first wait on them, at
+// clamped addresses: rows past N are never stored, and sign words past a row
+// meet ranks past R, whose t is zero.
 // ---------------------------------------------------------------------------
 template <typename YT, int MT, int S, int WAVES>
 __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p) {
@@ -791,9 +792,14 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   const int nc = nvalid ? n : 0;
   const int M = p.M;
   const bool two = P.nb > 1;
-  // half of the latent buffer the latent kernel of this call filled; only
-  // block 0 writes the state here, and only sync[0]
-  const uint32_t hq = p.sync[1] & 1u;
+  // half of the latent buffer the latent kernel of this call filled (only
+  // block 0 writes the state here, and only sync[0]).  Read first, with a
+  // vector load (the index is opaque to the compiler), so that the wait for it
+  // holds none of the loads issued after it
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const uint32_t hq_word = p.sync[1 + zero];
+  __builtin_amdgcn_sched_barrier(0);
 
   // the projection's steps in sequence and this wave's part [q0, q1) of them
   StepSeq sq;
@@ -811,11 +817,32 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   const int q0 = min(part * per, nsteps);
   const int q1 = min(q0 + per, nsteps);
 
-  // (1) this thread's first staging chunk: chunk q of the chunks of both
-  // branches in sequence, every stored row
+  // (1) sign words of the wave's steps
+  SignWords<S> sw;
+  sw.load(sq, nc, q0, q1, grp);
+  // (2) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
+  const float h0v = P.h[0][nc];
+  const float h1v = P.h[two ? 1 : 0][nc];
+  const float* __restrict__ bsrc = P.bias ? P.bias : P.h[0];
+  const float bnv = bsrc[nc];
+  const float* __restrict__ rsrc = P.res ? P.res : P.h[0];
+  const size_t rstride = P.res ? size_t(P.N) : 0;  // no residual: every load reads h[0][0]
+  const int rcol = P.res ? nc : 0;
+  float resv[L::MB][4];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      resv[mb][i] = rsrc[size_t(min(mb * 8 + (grp & 1) * 4 + i, M - 1)) * rstride + rcol];
+
+  // (3) this thread's first staging chunk: chunk q of the chunks of both
+  // branches in sequence, every stored row.  Issued last: its address needs
+  // the latent-buffer half, read from memory, so the loads that do not wait
+  // for that go first (the staging then waits for every load)
   const int nch0 = 4 * P.RWp[0];
   const int nch1 = two ? 4 * P.RWp[1] : 0;
   const int nch = nch0 + nch1;
+  const uint32_t hq = __builtin_amdgcn_readfirstlane(hq_word) & 1u;
   const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
   u32x4* tb0 = lds_t;
   u32x4* tb1 = lds_t + size_t(L::MB) * nch0 * L::ROWS;
@@ -869,26 +896,7 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
 #pragma unroll
   for (int i = 0; i < (MT + 7) / 8; ++i) ssq[i].load(ta + p.tsize + 8 * i);
 
-  // (2) sign words of the wave's steps
-  SignWords<S> sw;
-  sw.load(sq, nc, q0, q1, grp);
-  // (3) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
-  const float h0v = P.h[0][nc];
-  const float h1v = P.h[two ? 1 : 0][nc];
-  const float* __restrict__ bsrc = P.bias ? P.bias : P.h[0];
-  const float bnv = bsrc[nc];
-  const float* __restrict__ rsrc = P.res ? P.res : P.h[0];
-  const size_t rstride = P.res ? size_t(P.N) : 0;  // no residual: every load reads h[0][0]
-  const int rcol = P.res ? nc : 0;
-  float resv[L::MB][4];
-#pragma unroll
-  for (int mb = 0; mb < L::MB; ++mb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      resv[mb][i] = rsrc[size_t(min(mb * 8 + (grp & 1) * 4 + i, M - 1)) * rstride + rcol];
-
-  // (4) staging: the first chunk (waits for its loads only), then any chunks
-  // past the first THREADS
+  // (4) staging: the first chunk, then any chunks past the first THREADS
   {
     const bool late = p.late_rs != 0;
     const float kf = float(p.K), eps = p.eps;
