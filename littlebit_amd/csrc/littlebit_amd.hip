@@ -893,19 +893,23 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
   };
   Raw8<float> v[L::MB][L::MR];
   if (tid - lane < nch) load_chunk(min(tid, nch - 1), v);  // waves with no chunk skip
+  const bool late = p.late_rs != 0;
+  if (late) {
 #pragma unroll
-  for (int i = 0; i < (MT + 7) / 8; ++i) ssq[i].load(ta + p.tsize + 8 * i);
+    for (int i = 0; i < (MT + 7) / 8; ++i) ssq[i].load(ta + p.tsize + 8 * i);
+  }
 
   // (4) staging: the first chunk, then any chunks past the first THREADS
-  {
-    const bool late = p.late_rs != 0;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
+  if (late) {
     const float kf = float(p.K), eps = p.eps;
 #pragma unroll
     for (int i = 0; i < (MT + 7) / 8; ++i) {
       float a[8];
       ssq[i].get(a);
 #pragma unroll
-      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = late ? 1.f / sqrtf(a[e] / kf + eps) : 1.f;
+      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = 1.f / sqrtf(a[e] / kf + eps);
     }
   }
   if (tid < nch) put_chunk(tid, v);
