@@ -276,7 +276,14 @@ struct Compact {
 //   LBK_INPUT_SILU_MUL  x[m, k] / (1 + exp(-x[m, k])) * x1[m, k]
 // (the RMSNorm, SiLU * up and their order are those of the reference's CPU
 // decode step, patches/littlebit_cpu_optimized.cpp:1370-1438).
-__device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
+// SiLU with the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: about 1
+// ulp each).  An IEEE divide costs ~10 instructions, and the latent kernel
+// evaluates SiLU for its whole k-chunk in every row-block.
+__device__ __forceinline__ float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.f + __expf(-v)); }
+// 1 / sqrt(ssum / K + eps) with v_rsq_f32 (about 1 ulp), kinv = 1 / K
+__device__ __forceinline__ float inv_rms(float ssum, float kinv, float eps) {
+  return __builtin_amdgcn_rsqf(ssum * kinv + eps);
+}
 
 // rs[m] = 1 / sqrt(mean_k x[m, k]^2 + eps) from per-thread partial sums of
 // squares: shuffles within each wave, then one LDS pass.  Ends with a barrier.
@@ -296,7 +303,7 @@ __device__ __forceinline__ void rms_finish(float (&part)[MT], int K, float eps, 
   if (tid < MT) {
     float ssum = 0.f;
     for (int w = 0; w < BLOCK / 64; ++w) ssum += scratch[w * MT + tid];
-    rs[tid] = 1.f / sqrtf(ssum / float(K) + eps);
+    rs[tid] = inv_rms(ssum, 1.f / float(K), eps);
   }
   __syncthreads();
 }
@@ -903,13 +910,13 @@ __global__ __launch_bounds__(WAVES * kWave) void expand_mfma_kernel(MfmaParams p
 #pragma unroll
   for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
   if (late) {
-    const float kf = float(p.K), eps = p.eps;
+    const float kinv = 1.f / float(p.K), eps = p.eps;
 #pragma unroll
     for (int i = 0; i < (MT + 7) / 8; ++i) {
       float a[8];
       ssq[i].get(a);
 #pragma unroll
-      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = 1.f / sqrtf(a[e] / kf + eps);
+      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = inv_rms(a[e], kinv, eps);
     }
   }
   if (tid < nch) put_chunk(tid, v);
