@@ -1753,6 +1753,7 @@ struct Plan {
   int wsteps;    // expand_mfma_kernel unroll bound S
   int waves;     // expand_mfma_kernel waves per block (4 or 8)
   int splits;    // expand_mfma_kernel waves per 16-row tile
+  int chunk;     // > 0: rows per decode-path call, the call runs over chunks of rows
   size_t lds1, lds2;
   size_t ws_total;
 };
@@ -1842,7 +1843,7 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64
   return best;
 }
 
-Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
+Plan plan_one(const ProjDesc* pd, int np, int64_t M, int64_t K) {
   Plan pl{};
   int64_t nrb = 0, chunks_max = 0;
   size_t lds2 = 0;
@@ -1879,6 +1880,28 @@ Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
     pl.ws_total = kTOffset + kTBytes;
   } else {
     pl.ws_total = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
+  }
+  return pl;
+}
+
+// A few rows more than the decode path takes at once (or rows whose t does
+// not fit in LDS) run as decode-path calls over chunks of rows: the GEMM
+// path's 128-row tiles leave a handful of blocks per call at such M (e.g. 17
+// blocks for the latent stage of a Llama-2 o projection at M = 33).  Rows of
+// a call are independent, so the chunks compute what one call would.
+constexpr int64_t kMaxChunkedM = 64;
+
+Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K) {
+  Plan pl = plan_one(pd, np, M, K);
+  if (!pl.mfma && M > 1 && M <= kMaxChunkedM) {
+    for (int64_t c : {int64_t(16), int64_t(8)}) {
+      if (c >= M) continue;
+      Plan pc = plan_one(pd, np, c, K);
+      if (pc.mfma) {
+        pc.chunk = int(c);
+        return pc;
+      }
+    }
   }
   return pl;
 }
@@ -2122,6 +2145,26 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
   if (!workspace || workspace_bytes < pl.ws_total)
     return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.chunk > 0) {
+    const size_t xb = x_dtype == LBK_F32 ? 4 : 2, yb = y_dtype == LBK_F32 ? 4 : 2;
+    for (int64_t m0 = 0; m0 < M; m0 += pl.chunk) {
+      const int64_t mc = std::min<int64_t>(pl.chunk, M - m0);
+      ProjDesc pc[kMaxProj];
+      for (int q = 0; q < np; ++q) {
+        pc[q] = pd[q];
+        pc[q].y = static_cast<char*>(pd[q].y) + size_t(m0) * size_t(pd[q].N) * yb;
+        if (pd[q].res) pc[q].res = pd[q].res + size_t(m0) * size_t(pd[q].N);
+      }
+      InputDesc ic = in;
+      if (ic.x1) ic.x1 = static_cast<const char*>(in.x1) + size_t(m0) * size_t(K) * xb;
+      const Plan pm = plan_one(pc, np, mc, K);
+      if (!pm.mfma) return set_error(LBK_ERR_ARG, "a chunk of %lld rows has no decode-path plan", (long long)mc);
+      rc = forward_mfma(pc, np, pm, mc, K, static_cast<const char*>(x) + size_t(m0) * size_t(K) * xb, x_dtype, ic,
+                        y_dtype, workspace, s);
+      if (rc != LBK_OK) return rc;
+    }
+    return LBK_OK;
+  }
   if (pl.mfma) return forward_mfma(pd, np, pl, M, K, x, x_dtype, in, y_dtype, workspace, s);
   return forward_gemm(pd, np, M, K, x, x_dtype, in, y_dtype, workspace, s);
 }

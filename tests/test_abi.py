@@ -173,7 +173,10 @@ def test_group_workspace_query():
     one = lib.lbk_linear_workspace_bytes(br, 2, 8, 4096, 4096)
     grp = lib.lbk_group_workspace_bytes(arr, 3, 8, 4096)
     assert 0 < one <= grp
-    assert lib.lbk_group_workspace_bytes(arr, 3, 64, 4096) > grp  # general path: per-call latent buffers
+    # up to 64 rows: decode-path calls over chunks of rows, the same workspace
+    assert lib.lbk_group_workspace_bytes(arr, 3, 33, 4096) == grp
+    assert lib.lbk_group_workspace_bytes(arr, 3, 64, 4096) == grp
+    assert lib.lbk_group_workspace_bytes(arr, 3, 65, 4096) > grp  # GEMM path: per-call planes
     assert lib.lbk_group_workspace_bytes(arr, 0, 8, 4096) == 0
 
 

@@ -159,15 +159,26 @@ def test_prefill_bf16_llama3_shapes(gpu, M, K, N, ranks):
     _check(y, xu, brs, K, N, TOL_BF16_PREFILL, what=f"bf16 M={M} K={K} N={N} R={ranks}")
 
 
-@pytest.mark.parametrize("M,K,N,ranks", [(32, 4096, 4096, [205, 1843]), (17, 4096, 11008, [298, 2686]),
-                                         (64, 11008, 4096, [298, 2686]), (33, 70, 45, [37, 5]),
+@pytest.mark.parametrize("M,K,N,ranks", [(65, 4096, 4096, [205, 1843]), (96, 11008, 4096, [298, 2686]),
                                          (129, 1000, 300, [130]), (8, 4096, 4096, [4000, 4000])])
 def test_gemm_path_fp32(gpu, M, K, N, ranks):
-    """fp32 activations at M > 16 (tree verify) or with operands too large for
-    the decode kernels' LDS: hi/lo-split GEMM path, fp32 tolerance."""
+    """fp32 activations at M > 64 or with operands too large for the decode
+    kernels' LDS at any chunk of rows: hi/lo-split GEMM path, fp32 tolerance."""
     x, brs = _synthetic(1020 + M, M, K, N, ranks)
     y, xu = _run(gpu, x, brs)
     _check(y, xu, brs, K, N, TOL_F32, what=f"fp32 gemm M={M} K={K} N={N} R={ranks}")
+
+
+@pytest.mark.parametrize("M,K,N,ranks", [(32, 4096, 4096, [205, 1843]), (17, 4096, 11008, [298, 2686]),
+                                         (64, 11008, 4096, [298, 2686]), (33, 70, 45, [37, 5]),
+                                         (12, 4096, 11008, [298, 2686]), (41, 96, 130, [3])])
+def test_chunked_rows_fp32(gpu, M, K, N, ranks):
+    """17 <= M <= 64 (tree verify), and M <= 16 whose t does not fit the
+    decode kernels' LDS at once: decode-path calls over chunks of 16 or 8
+    rows, fp32 tolerance."""
+    x, brs = _synthetic(1020 + M, M, K, N, ranks)
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=f"fp32 chunked M={M} K={K} N={N} R={ranks}")
 
 
 def test_empty_batch(gpu):
