@@ -1672,6 +1672,221 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Attention of N new tokens (1 <= N <= 64) at positions start .. start+N-1
+// over the cache and themselves, causal or with a tree mask (a new token sees
+// every cached position and the new tokens its mask row marks, itself
+// included when the row says so).  The reference runs its batch forward
+// token by token (patches/littlebit_cpu_optimized.cpp:1846-2079) and its tree
+// verification through the model's attention with the tree mask
+// (tree_utils.py:72-214); here one launch covers all N tokens.
+// grid = (heads, chunks of ch positions), 256 threads = 4 waves: wave w
+// takes query tile w % qt (16 queries) and part w / qt of the chunk's
+// positions (qt * ps = 4).  Scores S^T = K Q^T and O^T += V^T P^T run on
+// v_mfma_f32_16x16x4_f32 over 16-position tiles, so products and sums stay
+// fp32; the exp(scores) come out of the score MFMA in the B layout the value
+// MFMA takes.  Rows at t >= start are read from the new k and v (the launch
+// also stores them into the cache, for later launches).  Online softmax per
+// query; the ps parts of a query tile meet in LDS, and one partial (max,
+// sum, o) per (head, chunk, query) goes to attn_batch_combine_kernel.
+// MFMA 16x16x4 f32 lanes: A[l % 16][l / 16], B[l / 16][l % 16], D[4 (l / 16)
+// + i][l % 16].
+// ---------------------------------------------------------------------------
+struct AttnBatchParams {
+  const float* q;         // [N][heads * HD], unscaled
+  const float* k;         // [N][kv_heads * HD] new keys
+  const float* v;         // [N][kv_heads * HD] new values
+  float* kc;              // [kv_heads][max_seq][HD]
+  float* vc;
+  const uint8_t* tree;    // [N][N]: row i marks the new tokens token i sees; null: causal
+  float* part;            // [heads][chunks][N][HD + 2]: o, max, sum
+  float* out;             // [N][heads * HD]
+  int64_t start;
+  int N, heads, kvh, rep, max_seq, chunks, ch, qt, ps;
+  float scale;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParams p) {
+  constexpr int DG = HD / 4;   // dims per lane group in the score MFMAs
+  constexpr int NT = HD / 16;  // 16-dim tiles of O^T: tile 4a + b holds dims 64a + 4r + b, r < 16
+  constexpr int NA = HD / 64;
+  __shared__ float red[3][16][HD + 2];
+  const int h = int(blockIdx.x), c = int(blockIdx.y), tid = int(threadIdx.x);
+  const int wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, g = lane >> 4;
+  const int kv = h / p.rep;
+  const int N = p.N;
+  const int st = int(p.start);
+  const int S = st + N;
+  const int t0 = c * p.ch, t1 = min(t0 + p.ch, S);
+  const size_t nstride = size_t(p.kvh) * HD;  // row stride of the new k and v
+  float* kcache = p.kc + size_t(kv) * p.max_seq * HD;
+  float* vcache = p.vc + size_t(kv) * p.max_seq * HD;
+  const float* knew = p.k + size_t(kv) * HD;
+  const float* vnew = p.v + size_t(kv) * HD;
+
+  // the chunk's new rows into the cache (one head of each kv group stores)
+  if (h % p.rep == 0) {
+    const int n0 = max(t0, st), n1 = min(t1, S);
+    for (int i = tid; i < (n1 - n0) * HD; i += kAttnThreads) {
+      const int t = n0 + i / HD, d = i % HD;
+      kcache[size_t(t) * HD + d] = knew[size_t(t - st) * nstride + d];
+      vcache[size_t(t) * HD + d] = vnew[size_t(t - st) * nstride + d];
+    }
+  }
+
+  const int qtile = wave % p.qt, part = wave / p.qt;
+  const int qi = qtile * 16 + col;  // this lane's query: column col of the score tile
+  const bool qvalid = qi < N;
+  float qv[DG];
+  {
+    const float* qr = p.q + (size_t(min(qi, N - 1)) * p.heads + h) * HD + g * DG;
+#pragma unroll
+    for (int j = 0; j < DG / 4; ++j) {
+      const float4 f = *reinterpret_cast<const float4*>(qr + 4 * j);
+      qv[4 * j] = f.x * p.scale;
+      qv[4 * j + 1] = f.y * p.scale;
+      qv[4 * j + 2] = f.z * p.scale;
+      qv[4 * j + 3] = f.w * p.scale;
+    }
+  }
+  const int P = p.ch / p.ps;
+  const int w0 = t0 + part * P, w1 = min(w0 + P, t1);
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[NT];
+#pragma unroll
+  for (int dt = 0; dt < NT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = w0; s0 < w1; s0 += 16) {
+    // K row s0 + col, dims g*DG .. +DG (A of the score MFMAs); V rows
+    // s0 + 4g + i, dims 64a + 4col .. +4 (A of the value MFMAs); positions
+    // past w1 read row w1 - 1 and are masked
+    float kk[DG];
+    {
+      const int t = min(s0 + col, w1 - 1);
+      const float* kr = (t < st ? kcache + size_t(t) * HD : knew + size_t(t - st) * nstride) + g * DG;
+#pragma unroll
+      for (int j = 0; j < DG / 4; ++j) {
+        const float4 f = *reinterpret_cast<const float4*>(kr + 4 * j);
+        kk[4 * j] = f.x;
+        kk[4 * j + 1] = f.y;
+        kk[4 * j + 2] = f.z;
+        kk[4 * j + 3] = f.w;
+      }
+    }
+    float4 vv[4][NA];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(s0 + 4 * g + i, w1 - 1);
+      const float* vr = t < st ? vcache + size_t(t) * HD : vnew + size_t(t - st) * nstride;
+#pragma unroll
+      for (int a = 0; a < NA; ++a) vv[i][a] = *reinterpret_cast<const float4*>(vr + 64 * a + 4 * col);
+    }
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DG; ++j) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j], qv[j], sc, 0, 0, 0);
+    // sc[i] = score of position s0 + 4g + i for query qi
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = s0 + 4 * g + i;
+      bool ok = qvalid && t < w1;
+      if (ok && t >= st) ok = p.tree ? p.tree[size_t(qi) * N + (t - st)] != 0 : t - st <= qi;
+      sv[i] = ok ? sc[i] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    const bool none = mn == -INFINITY;  // nothing visible yet: keep zeros
+    const float corr = none ? 1.f : __expf(m - mn);
+    float pv[4], ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pv[i] = none ? 0.f : __expf(sv[i] - mn);
+      ls += pv[i];
+    }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    l = l * corr + ls;
+    m = mn;
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt) {
+      o[dt] *= corr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 w = vv[i][dt / 4];
+        const float a = (dt % 4) == 0 ? w.x : (dt % 4) == 1 ? w.y : (dt % 4) == 2 ? w.z : w.w;
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pv[i], o[dt], 0, 0, 0);
+      }
+    }
+  }
+  // o[dt][j] = O^T[dim 64 (dt / 4) + 16 g + 4 j + dt % 4][qi]
+  auto dim_of = [&](int dt, int j) { return 64 * (dt / 4) + 16 * g + 4 * j + (dt % 4); };
+  if (p.ps > 1) {
+    if (part > 0) {
+      const int slot = qtile + p.qt * (part - 1);
+#pragma unroll
+      for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[slot][col][dim_of(dt, j)] = o[dt][j];
+      if (g == 0) {
+        red[slot][col][HD] = m;
+        red[slot][col][HD + 1] = l;
+      }
+    }
+    __syncthreads();
+    if (part == 0) {
+      for (int pi = 1; pi < p.ps; ++pi) {
+        const int slot = qtile + p.qt * (pi - 1);
+        const float mo = red[slot][col][HD], lo = red[slot][col][HD + 1];
+        const float mn = fmaxf(m, mo);
+        const float a = m == -INFINITY ? 0.f : __expf(m - mn);
+        const float b = mo == -INFINITY ? 0.f : __expf(mo - mn);
+        l = l * a + lo * b;
+#pragma unroll
+        for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[dt][j] = o[dt][j] * a + red[slot][col][dim_of(dt, j)] * b;
+        m = mn;
+      }
+    }
+  }
+  if (part == 0 && qvalid) {
+    float* pp = p.part + ((size_t(h) * p.chunks + c) * N + qi) * (HD + 2);
+#pragma unroll
+    for (int dt = 0; dt < NT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pp[dim_of(dt, j)] = o[dt][j];
+    if (g == 0) {
+      pp[HD] = m;
+      pp[HD + 1] = l;
+    }
+  }
+}
+
+// out[qi][h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c over
+// the chunks' partials, one pass with a running maximum.  grid = (heads, N).
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams p) {
+  const int h = int(blockIdx.x), qi = int(blockIdx.y), d = int(threadIdx.x);
+  const size_t cstride = size_t(p.N) * (HD + 2);
+  const float* pp = p.part + (size_t(h) * p.chunks * p.N + qi) * (HD + 2);
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int c = 0; c < p.chunks; ++c) {
+    const float* pc = pp + size_t(c) * cstride;
+    const float mc = pc[HD];
+    if (mc == -INFINITY) continue;  // nothing this query sees in the chunk
+    const float lc = pc[HD + 1], oc = pc[d];
+    const float Mn = fmaxf(M, mc);
+    const float a = M == -INFINITY ? 0.f : __expf(M - Mn), b = __expf(mc - Mn);
+    num = num * a + oc * b;
+    den = den * a + lc * b;
+    M = Mn;
+  }
+  p.out[(size_t(qi) * p.heads + h) * HD + d] = num / den;
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -2306,6 +2521,72 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   if (head_dim == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(heads), dim3(128), 0, s, p);
   else hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(heads), dim3(64), 0, s, p);
   return check_launch("attn_combine_kernel");
+}
+
+// Positions per block of attn_batch_kernel: 64 for up to 16 new tokens,
+// else 128 (so that the partials stay small next to the K and V read),
+// doubled while the grid would exceed 2048 blocks.
+static int attn_batch_ch(int heads, int n, int64_t start) {
+  int ch = n <= 16 ? 64 : 128;
+  while (ch < 4096 && int64_t(heads) * ceil_div(start + n, ch) > 2048) ch *= 2;
+  return ch;
+}
+
+size_t lbk_attention_batch_partial_bytes(int heads, int n, int64_t start, int head_dim) {
+  if (heads < 1 || n < 1 || start < 0 || head_dim < 1) return 0;
+  const int64_t chunks = ceil_div(start + n, attn_batch_ch(heads, n, start));
+  return size_t(heads) * size_t(chunks) * size_t(n) * size_t(head_dim + 2) * sizeof(float);
+}
+
+int lbk_attention_batch(const float* q, const float* k, const float* v, float* k_cache, float* v_cache, int n,
+                        int heads, int kv_heads, int head_dim, int max_seq, int64_t start, const uint8_t* tree_mask,
+                        float scale, float* partial, size_t partial_bytes, float* out, void* stream) {
+  g_last_error[0] = '\0';
+  if (n < 1 || n > 64) return set_error(LBK_ERR_ARG, "n must be in [1, 64], got %d", n);
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0)
+    return set_error(LBK_ERR_ARG, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv_heads);
+  if (head_dim != 64 && head_dim != 128) return set_error(LBK_ERR_ARG, "head_dim must be 64 or 128, got %d", head_dim);
+  if (max_seq < 1 || max_seq > (1 << 24)) return set_error(LBK_ERR_ARG, "max_seq out of range: %d", max_seq);
+  if (start < 0 || start + n > max_seq)
+    return set_error(LBK_ERR_ARG, "positions %lld .. %lld outside [0, %d)", (long long)start, (long long)(start + n - 1),
+                     max_seq);
+  if (!q || !k || !v || !k_cache || !v_cache || !out || !partial) return set_error(LBK_ERR_ARG, "NULL pointer");
+  for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
+                          static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
+    if (!aligned16(ptr)) return set_error(LBK_ERR_ARG, "q, k, v and the caches must be 16-byte aligned");
+  const size_t need = lbk_attention_batch_partial_bytes(heads, n, start, head_dim);
+  if (partial_bytes < need)
+    return set_error(LBK_ERR_WORKSPACE, "partial buffer of %zu bytes needed, %zu given", need, partial_bytes);
+  AttnBatchParams p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.tree = tree_mask;
+  p.part = partial;
+  p.out = out;
+  p.start = start;
+  p.N = n;
+  p.heads = heads;
+  p.kvh = kv_heads;
+  p.rep = heads / kv_heads;
+  p.max_seq = max_seq;
+  p.ch = attn_batch_ch(heads, n, start);
+  p.chunks = int(ceil_div(start + n, p.ch));
+  p.qt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
+  p.ps = 4 / p.qt;
+  p.scale = scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid{unsigned(heads), unsigned(p.chunks), 1u};
+  if (head_dim == 128) hipLaunchKernelGGL(attn_batch_kernel<128>, grid, dim3(kAttnThreads), 0, s, p);
+  else hipLaunchKernelGGL(attn_batch_kernel<64>, grid, dim3(kAttnThreads), 0, s, p);
+  int rc = check_launch("attn_batch_kernel");
+  if (rc != LBK_OK) return rc;
+  const dim3 cgrid{unsigned(heads), unsigned(n), 1u};
+  if (head_dim == 128) hipLaunchKernelGGL(attn_batch_combine_kernel<128>, cgrid, dim3(128), 0, s, p);
+  else hipLaunchKernelGGL(attn_batch_combine_kernel<64>, cgrid, dim3(64), 0, s, p);
+  return check_launch("attn_batch_combine_kernel");
 }
 
 }  // extern "C"

@@ -143,12 +143,14 @@ class LittleBitDecoder:
         self.k_cache = torch.zeros(shape, dtype=torch.float32, device=dev)
         self.v_cache = torch.zeros(shape, dtype=torch.float32, device=dev)
         self.cache_pos = 0
-        # one-token steps use the HIP decode attention (head_dim 64 or 128)
+        # one-token steps and batches of up to 64 tokens use the HIP attention
+        # (head_dim 64 or 128)
         self._hip_attn = self.fuse and c.head_dim in (64, 128)
         if self._hip_attn:
             from . import _lib
             nbytes = _lib.load().lbk_attention_partial_bytes(c.num_attention_heads, self.max_seq_len, c.head_dim)
             self._attn_part = torch.empty(max(int(nbytes) // 4, 1), dtype=torch.float32, device=dev)
+        self._batch_part = None  # partials of the batched attention, grown as needed
 
     def reset(self):
         """Forget the cached positions (the reference's _LBModelUnit.reset)."""
@@ -170,6 +172,8 @@ class LittleBitDecoder:
         kc, vc = self.k_cache[li], self.v_cache[li]
         if N == 1 and tree_mask is None and self._hip_attn:
             return self._attention_hip(q, k, v, kc, vc, start, pos_t)
+        if 1 < N <= 64 and pos_t is None and self._hip_attn and length == start + N:
+            return self._attention_batch_hip(q, k, v, kc, vc, start, tree_mask)
         k3 = k.view(N, kvh, hd).transpose(0, 1)
         v3 = v.view(N, kvh, hd).transpose(0, 1)
         if pos_t is None:
@@ -213,6 +217,28 @@ class LittleBitDecoder:
             int(start), float(c.attn_scale), self._attn_part.data_ptr(), self._attn_part.numel() * 4, out.data_ptr(),
             torch.cuda.current_stream(q.device).cuda_stream)
         _lib.check(rc, "lbk_attention_decode")
+        return out
+
+    def _attention_batch_hip(self, q, k, v, kc, vc, start: int, tree_mask: Optional[torch.Tensor]):
+        """N new tokens in one launch pair (causal or ``tree_mask``)."""
+        from . import _lib
+        c = self.config
+        N = q.shape[0]
+        lib = _lib.load()
+        need = int(lib.lbk_attention_batch_partial_bytes(c.num_attention_heads, N, int(start), c.head_dim))
+        if self._batch_part is None or self._batch_part.numel() * 4 < need:
+            self._batch_part = torch.empty(max(need // 4, 1), dtype=torch.float32, device=q.device)
+        out = torch.empty((N, c.num_attention_heads * c.head_dim), dtype=torch.float32, device=q.device)
+        q, k, v = (t.to(torch.float32).contiguous() for t in (q, k, v))
+        tm = None
+        if tree_mask is not None:
+            tm = tree_mask.to(device=q.device, dtype=torch.uint8).contiguous()
+        rc = lib.lbk_attention_batch(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), N, c.num_attention_heads,
+            c.num_key_value_heads, c.head_dim, self.max_seq_len, int(start), None if tm is None else tm.data_ptr(),
+            float(c.attn_scale), self._batch_part.data_ptr(), self._batch_part.numel() * 4, out.data_ptr(),
+            torch.cuda.current_stream(q.device).cuda_stream)
+        _lib.check(rc, "lbk_attention_batch")
         return out
 
     def forward_hidden(self, x: torch.Tensor, start: int, length: Optional[int] = None,

@@ -141,6 +141,68 @@ def test_attention_decode_rejects_bad_args(gpu):
     assert lib.lbk_attention_decode(p, p, p, p, p, 4, 4, 64, 300, None, 0, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("n,heads,kvh,hd,max_seq,start,tree", [
+    (2, 4, 4, 64, 64, 0, False), (8, 32, 32, 128, 1100, 1024, False), (16, 8, 2, 128, 200, 100, False),
+    (17, 8, 8, 64, 80, 37, True), (33, 32, 32, 128, 1100, 1024, True), (64, 4, 1, 128, 600, 500, False),
+    (5, 4, 2, 64, 16, 3, True), (40, 2, 2, 64, 40, 0, False)])
+def test_attention_batch_kernel(gpu, n, heads, kvh, hd, max_seq, start, tree):
+    """lbk_attention_batch against float64: token i at start + i attends to
+    every cached position and the new tokens j <= i (or its tree-mask row),
+    the new k/v stored into the cache."""
+    import littlebit_amd._lib as L
+    g = torch.Generator(device="cpu").manual_seed(n * 131 + start)
+    kc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    vc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    q = torch.randn((n, heads * hd), generator=g).to(gpu)
+    k = torch.randn((n, kvh * hd), generator=g).to(gpu)
+    v = torch.randn((n, kvh * hd), generator=g).to(gpu)
+    if tree:
+        mask = torch.rand((n, n), generator=g) < 0.5
+        mask |= torch.eye(n, dtype=torch.bool)
+    else:
+        mask = torch.tril(torch.ones((n, n), dtype=torch.bool))
+    scale = hd ** -0.5
+    K = torch.cat([kc[:, :start].double().cpu(), k.view(n, kvh, hd).transpose(0, 1).double().cpu()], dim=1)
+    V = torch.cat([vc[:, :start].double().cpu(), v.view(n, kvh, hd).transpose(0, 1).double().cpu()], dim=1)
+    rep = heads // kvh
+    allowed = torch.cat([torch.ones((n, start), dtype=torch.bool), mask], dim=1)  # [n, start + n]
+    qd = q.view(n, kvh, rep, hd).double().cpu()
+    s = torch.einsum("ngrd,gtd->ngrt", qd, K) * scale
+    s = s.masked_fill(~allowed.view(n, 1, 1, start + n), float("-inf"))
+    ref = torch.einsum("ngrt,gtd->ngrd", torch.softmax(s, dim=-1), V).reshape(n, heads * hd)
+    lib = L.load()
+    part = torch.empty(lib.lbk_attention_batch_partial_bytes(heads, n, start, hd) // 4 + 1, device=gpu)
+    out = torch.full((n, heads * hd), float("nan"), device=gpu)
+    tm = mask.to(torch.uint8).to(gpu) if tree else None
+    old_k = kc.clone()
+    print(f"[attention_batch] n={n} heads={heads} kvh={kvh} hd={hd} start={start} tree={tree}", flush=True)
+    rc = lib.lbk_attention_batch(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), n, heads,
+                                 kvh, hd, max_seq, start, None if tm is None else tm.data_ptr(), scale, part.data_ptr(),
+                                 part.numel() * 4, out.data_ptr(), None)
+    L.check(rc, "lbk_attention_batch")
+    torch.cuda.synchronize()
+    err = O.rel_err(out.cpu().numpy(), ref.numpy())
+    print(f"[attention_batch] rel_err={err:.2e}", flush=True)
+    assert err <= 1e-5
+    assert torch.equal(kc[:, start:start + n], k.view(n, kvh, hd).transpose(0, 1))
+    assert torch.equal(vc[:, start:start + n], v.view(n, kvh, hd).transpose(0, 1))
+    assert torch.equal(kc[:, :start], old_k[:, :start]) and torch.equal(kc[:, start + n:], old_k[:, start + n:])
+
+
+def test_attention_batch_rejects_bad_args(gpu):
+    import littlebit_amd._lib as L
+    lib = L.load()
+    x = torch.zeros(1 << 16, device=gpu)
+    p = x.data_ptr()
+    big = x.numel() * 4
+    assert lib.lbk_attention_batch(p, p, p, p, p, 65, 4, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 6, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 96, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, 121, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p + 4, p, p, p, p, 8, 4, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, 0, None, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
+
+
 def test_batch_equals_token_by_token(gpu):
     from littlebit_amd.decode import LittleBitDecoder
     cfg = _cfg()
