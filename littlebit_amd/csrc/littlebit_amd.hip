@@ -1479,7 +1479,7 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
 // attn_combine_kernel merges.  pos is read on the device when pos_ptr is set (graph replay);
 // pos >= max_seq writes nothing but zeros to out.
 // ---------------------------------------------------------------------------
-constexpr int kAttnChunk = 32;
+constexpr int kAttnChunk = 16;  // positions per block: more, smaller blocks measured faster at KV 512 than 32 or 64
 constexpr int kAttnThreads = 256;
 
 struct AttnParams {
@@ -1532,7 +1532,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
     kc[size_t(pos) * HD + tid] = kn[tid];
     vc[size_t(pos) * HD + tid] = vn[tid];
   }
-  __shared__ float qs[HD];
   __shared__ float ps[kAttnChunk];
   __shared__ float wred[NW];
   __shared__ float ored[NW][HD];
@@ -1552,10 +1551,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
       }
     }
   }
-  if (tid < HD) qs[tid] = p.q[size_t(h) * HD + tid] * p.scale;
-  __syncthreads();
+  // each lane's 4 query dims straight from memory (no LDS, no barrier), so
+  // the K loads below issue right behind it
   const int sub = lane / LPR, dl = (lane % LPR) * 4;
-  const float4 q4 = *reinterpret_cast<const float4*>(qs + dl);
+  float4 q4 = *reinterpret_cast<const float4*>(p.q + size_t(h) * HD + dl);
+  q4.x *= p.scale;
+  q4.y *= p.scale;
+  q4.z *= p.scale;
+  q4.w *= p.scale;
   if (full) {  // every load first, then the arithmetic
     float4 kk[PW / RPI];
 #pragma unroll
@@ -2493,6 +2496,9 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   if (!pos_device && (pos < 0 || pos >= max_seq))
     return set_error(LBK_ERR_ARG, "pos %lld outside [0, %d)", (long long)pos, max_seq);
   if (!q || !k || !v || !k_cache || !v_cache || !out) return set_error(LBK_ERR_ARG, "NULL pointer");
+  for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
+                          static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
+    if (!aligned16(ptr)) return set_error(LBK_ERR_ARG, "q, k, v and the caches must be 16-byte aligned");
   const int chunks = int(ceil_div(max_seq, kAttnChunk));
   const size_t need = lbk_attention_partial_bytes(heads, max_seq, head_dim);
   if (chunks > 1 && (!partial || partial_bytes < need))
