@@ -1651,8 +1651,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
   }
 }
 
-// out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c, in one pass
-// with a running maximum (each step rescales what it has).  grid = heads.
+// out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c, M the
+// largest m_c: one pass for M, one for the sums, so that every chunk's loads
+// are independent (a running maximum would chain them).  grid = heads.
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
   const int h = int(blockIdx.x), d = int(threadIdx.x);
@@ -1660,16 +1661,16 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
   if (pos < 0 || pos >= p.max_seq) return;  // out was zeroed by attn_decode_kernel
   const float* part = p.part + size_t(h) * p.chunks * (HD + 2);
   const int used = int(pos / kAttnChunk) + 1;  // chunks past pos hold empty partials
-  float M = -INFINITY, num = 0.f, den = 0.f;
-#pragma unroll 4
+  float M = -INFINITY;
+#pragma unroll 8
+  for (int c = 0; c < used; ++c) M = fmaxf(M, part[size_t(c) * (HD + 2) + HD]);
+  float num = 0.f, den = 0.f;
+#pragma unroll 8
   for (int c = 0; c < used; ++c) {
     const float* pc = part + size_t(c) * (HD + 2);
-    const float mc = pc[HD], lc = pc[HD + 1], oc = pc[d];
-    const float Mn = fmaxf(M, mc);
-    const float a = __expf(M - Mn), b = __expf(mc - Mn);  // M = -inf at first: a = 0
-    num = num * a + oc * b;
-    den = den * a + lc * b;
-    M = Mn;
+    const float w = __expf(pc[HD] - M);  // chunk 0 holds position 0, so M is finite
+    num += pc[d] * w;
+    den += pc[HD + 1] * w;
   }
   p.out[size_t(h) * HD + d] = num / den;
 }
@@ -1759,11 +1760,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
   f32x4 o[NT];
 #pragma unroll
   for (int dt = 0; dt < NT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s0 = w0; s0 < w1; s0 += 16) {
-    // K row s0 + col, dims g*DG .. +DG (A of the score MFMAs); V rows
-    // s0 + 4g + i, dims 64a + 4col .. +4 (A of the value MFMAs); positions
-    // past w1 read row w1 - 1 and are masked
-    float kk[DG];
+  // K row s0 + col, dims g*DG .. +DG (A of the score MFMAs); V rows
+  // s0 + 4g + i, dims 64a + 4col .. +4 (A of the value MFMAs); positions
+  // past w1 read row w1 - 1 and are masked.  The next tile's rows load while
+  // this tile computes.
+  auto load_kv = [&](int s0, float (&kk)[DG], float4 (&vv)[4][NA]) {
     {
       const int t = min(s0 + col, w1 - 1);
       const float* kr = (t < st ? kcache + size_t(t) * HD : knew + size_t(t - st) * nstride) + g * DG;
@@ -1776,7 +1777,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
         kk[4 * j + 3] = f.w;
       }
     }
-    float4 vv[4][NA];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = min(s0 + 4 * g + i, w1 - 1);
@@ -1784,9 +1784,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
 #pragma unroll
       for (int a = 0; a < NA; ++a) vv[i][a] = *reinterpret_cast<const float4*>(vr + 64 * a + 4 * col);
     }
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+  };
+  float kk[DG];
+  float4 vv[4][NA];
+  if (w0 < w1) load_kv(w0, kk, vv);
+  for (int s0 = w0; s0 < w1; s0 += 16) {
+    float kn[DG];
+    float4 vn[4][NA];
+    const bool more = s0 + 16 < w1;
+    if (more) load_kv(s0 + 16, kn, vn);
+    // four independent accumulator chains over the dims, then their sum
+    f32x4 sc4[4];
 #pragma unroll
-    for (int j = 0; j < DG; ++j) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j], qv[j], sc, 0, 0, 0);
+    for (int u = 0; u < 4; ++u) sc4[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DG; ++j) sc4[j % 4] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[j], qv[j], sc4[j % 4], 0, 0, 0);
+    const f32x4 sc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
     // sc[i] = score of position s0 + 4g + i for query qi
     float sv[4];
 #pragma unroll
@@ -1821,6 +1834,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
         const float a = (dt % 4) == 0 ? w.x : (dt % 4) == 1 ? w.y : (dt % 4) == 2 ? w.z : w.w;
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, pv[i], o[dt], 0, 0, 0);
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < DG; ++j) kk[j] = kn[j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int a = 0; a < NA; ++a) vv[i][a] = vn[i][a];
     }
   }
   // o[dt][j] = O^T[dim 64 (dt / 4) + 16 g + 4 j + dt % 4][qi]
@@ -1868,23 +1889,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
 }
 
 // out[qi][h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c over
-// the chunks' partials, one pass with a running maximum.  grid = (heads, N).
+// the chunks' partials, M the largest m_c (two passes, independent loads);
+// chunks where the query sees nothing hold m_c = -inf.  grid = (heads, N).
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams p) {
   const int h = int(blockIdx.x), qi = int(blockIdx.y), d = int(threadIdx.x);
   const size_t cstride = size_t(p.N) * (HD + 2);
   const float* pp = p.part + (size_t(h) * p.chunks * p.N + qi) * (HD + 2);
-  float M = -INFINITY, num = 0.f, den = 0.f;
+  float M = -INFINITY;
+#pragma unroll 8
+  for (int c = 0; c < p.chunks; ++c) M = fmaxf(M, pp[size_t(c) * cstride + HD]);
+  float num = 0.f, den = 0.f;
+#pragma unroll 8
   for (int c = 0; c < p.chunks; ++c) {
     const float* pc = pp + size_t(c) * cstride;
     const float mc = pc[HD];
-    if (mc == -INFINITY) continue;  // nothing this query sees in the chunk
-    const float lc = pc[HD + 1], oc = pc[d];
-    const float Mn = fmaxf(M, mc);
-    const float a = M == -INFINITY ? 0.f : __expf(M - Mn), b = __expf(mc - Mn);
-    num = num * a + oc * b;
-    den = den * a + lc * b;
-    M = Mn;
+    const float w = mc == -INFINITY ? 0.f : __expf(mc - M);
+    num += pc[d] * w;
+    den += pc[HD + 1] * w;
   }
   p.out[(size_t(qi) * p.heads + h) * HD + d] = num / den;
 }
@@ -2529,11 +2551,12 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   return check_launch("attn_combine_kernel");
 }
 
-// Positions per block of attn_batch_kernel: 64 for up to 16 new tokens,
-// else 128 (so that the partials stay small next to the K and V read),
+// Positions per block of attn_batch_kernel: 128 (so that the partials stay
+// small next to the K and V read, and waves of up to 16 tokens walk two
+// tiles, the second loading during the first; 64 measured slower at KV 1024),
 // doubled while the grid would exceed 2048 blocks.
 static int attn_batch_ch(int heads, int n, int64_t start) {
-  int ch = n <= 16 ? 64 : 128;
+  int ch = 128;
   while (ch < 4096 && int64_t(heads) * ceil_div(start + n, ch) > 2048) ch *= 2;
   return ch;
 }
