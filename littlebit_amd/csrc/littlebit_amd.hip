@@ -1991,7 +1991,7 @@ struct Plan {
   int nkc;       // k-chunks
   int nrb;       // row-blocks over all segments
   int wsteps;    // expand_mfma_kernel unroll bound S
-  int waves;     // expand_mfma_kernel waves per block (4 or 8)
+  int waves;     // expand_mfma_kernel waves per block (4, 8 or 12)
   int splits;    // expand_mfma_kernel waves per 16-row tile
   int chunk;     // > 0: rows per decode-path call, the call runs over chunks of rows
   size_t lds1, lds2;
@@ -2033,7 +2033,7 @@ struct ExpandChoice {
   int waves = 0, splits = 0, ws = 0;  // waves 0: no shape fits
 };
 
-// Expand launch shape: waves per block (4 or 8) and waves per 16-row tile
+// Expand launch shape: waves per block (4, 8 or 12) and waves per 16-row tile
 // (splits), by an estimate of the kernel's critical path in rank steps of one
 // wave: every pass of the t staging (a round trip to L2) weighs 8 steps and
 // repeats for each round of blocks the CUs cannot hold at once (blocks per
@@ -2057,12 +2057,14 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, size_t lds2, int64
   ExpandChoice best;
   int64_t best_key[2] = {INT64_MAX, INT64_MAX};
   const int64_t mb = (mt + 7) / 8;
-  for (int waves : {4, 8}) {
+  for (int waves : {4, 8, 12}) {
+    if (waves == 12 && mt > 8) continue;  // 12 waves of the M = 16 kernel spill
     const int threads = waves * kWave;
     const size_t lds = lds2 + expand_static_lds(waves, mt);
     if (lds > size_t(kMaxBlockLds)) continue;
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(int64_t(kLdsPerCU) / int64_t(lds), 2048 / threads));
     for (int splits = 1; splits <= waves; splits *= 2) {
+      if (waves % splits) continue;
       int64_t ws = 0;
       for (int q = 0; q < np; ++q) ws = std::max(ws, part_steps(pd[q], splits));
       if (ws > kMaxWaveSteps) continue;
@@ -2178,6 +2180,12 @@ void launch_expand_mfma(const MfmaParams& p, int grid, size_t lds, hipStream_t s
 
 template <typename YT, int MT, int S>
 void dispatch_expand_waves(const MfmaParams& p, int waves, int grid, size_t lds, hipStream_t s) {
+  if constexpr (MT <= 8) {
+    if (waves == 12) {
+      launch_expand_mfma<YT, MT, S, 12>(p, grid, lds, s);
+      return;
+    }
+  }
   if (waves == 8) launch_expand_mfma<YT, MT, S, 8>(p, grid, lds, s);
   else launch_expand_mfma<YT, MT, S, 4>(p, grid, lds, s);
 }
