@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 3
+#define LBK_ABI_VERSION 4
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -174,17 +174,20 @@ int lbk_attention_decode(const float* q, const float* k, const float* v,
  * (uint8 [n][n]).  q [n][heads * head_dim], k, v [n][kv_heads * head_dim]
  * (the new keys and values, also stored into k_cache / v_cache
  * [kv_heads][max_seq][head_dim]); q, k, v and the caches 16-byte aligned;
- * out [n][heads * head_dim].  partial: scratch of
- * lbk_attention_batch_partial_bytes().  Replaces the attention of the
+ * out [n][heads * head_dim].  start is read from start_device when that is
+ * not NULL (a captured graph then follows a position the device advances;
+ * a start with positions outside [0, max_seq) stores nothing and yields
+ * zeros).  partial: scratch of lbk_attention_batch_partial_bytes(heads, n,
+ * start, head_dim), with start = max_seq - n for a device start.  Replaces the attention of the
  * batched decode step (patches/littlebit_cpu_optimized.cpp:1846-2079) and the
  * tree-masked attention of tree verification (tree_utils.py:72-214). */
 size_t lbk_attention_batch_partial_bytes(int heads, int n, int64_t start, int head_dim);
 int lbk_attention_batch(const float* q, const float* k, const float* v,
                         float* k_cache, float* v_cache, int n, int heads,
                         int kv_heads, int head_dim, int max_seq,
-                        int64_t start, const uint8_t* tree_mask, float scale,
-                        float* partial, size_t partial_bytes, float* out,
-                        void* stream);
+                        const int64_t* start_device, int64_t start,
+                        const uint8_t* tree_mask, float scale, float* partial,
+                        size_t partial_bytes, float* out, void* stream);
 
 /* Expand packed signs to int8 {-1,+1}: out [rows, cols].
  * Replaces binary_unpacker (quantization/utils/binary_packer.py:54-97). */

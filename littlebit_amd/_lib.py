@@ -112,8 +112,8 @@ SIGNATURES = {
     "lbk_attention_batch_partial_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, _I64, ctypes.c_int]),
     "lbk_attention_batch": (
         ctypes.c_int,
-        [_VP, _VP, _VP, _VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _I64, _VP,
-         ctypes.c_float, _VP, ctypes.c_size_t, _VP, _VP],
+        [_VP, _VP, _VP, _VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP, _I64,
+         _VP, ctypes.c_float, _VP, ctypes.c_size_t, _VP, _VP],
     ),
     "lbk_unpack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
     "lbk_pack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),

@@ -1704,6 +1704,7 @@ struct AttnBatchParams {
   const uint8_t* tree;    // [N][N]: row i marks the new tokens token i sees; null: causal
   float* part;            // [heads][chunks][N][HD + 2]: o, max, sum
   float* out;             // [N][heads * HD]
+  const int64_t* start_ptr;  // start read on the device when set (graph replay), else `start`
   int64_t start;
   int N, heads, kvh, rep, max_seq, chunks, ch, qt, ps;
   float scale;
@@ -1720,7 +1721,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
   const int col = lane & 15, g = lane >> 4;
   const int kv = h / p.rep;
   const int N = p.N;
-  const int st = int(p.start);
+  const int64_t start = p.start_ptr ? *p.start_ptr : p.start;
+  if (start < 0 || start + N > p.max_seq) return;  // out of range: nothing read or stored (the combine writes zeros)
+  const int st = int(start);
   const int S = st + N;
   const int t0 = c * p.ch, t1 = min(t0 + p.ch, S);
   const size_t nstride = size_t(p.kvh) * HD;  // row stride of the new k and v
@@ -1894,6 +1897,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams p) {
   const int h = int(blockIdx.x), qi = int(blockIdx.y), d = int(threadIdx.x);
+  const int64_t start = p.start_ptr ? *p.start_ptr : p.start;
+  if (start < 0 || start + p.N > p.max_seq) {
+    p.out[(size_t(qi) * p.heads + h) * HD + d] = 0.f;
+    return;
+  }
   const size_t cstride = size_t(p.N) * (HD + 2);
   const float* pp = p.part + (size_t(h) * p.chunks * p.N + qi) * (HD + 2);
   float M = -INFINITY;
@@ -2571,27 +2579,32 @@ static int attn_batch_ch(int heads, int n, int64_t start) {
 
 size_t lbk_attention_batch_partial_bytes(int heads, int n, int64_t start, int head_dim) {
   if (heads < 1 || n < 1 || start < 0 || head_dim < 1) return 0;
+  // (with a device start, pass max_seq - n: the grid then covers every start)
   const int64_t chunks = ceil_div(start + n, attn_batch_ch(heads, n, start));
   return size_t(heads) * size_t(chunks) * size_t(n) * size_t(head_dim + 2) * sizeof(float);
 }
 
 int lbk_attention_batch(const float* q, const float* k, const float* v, float* k_cache, float* v_cache, int n,
-                        int heads, int kv_heads, int head_dim, int max_seq, int64_t start, const uint8_t* tree_mask,
-                        float scale, float* partial, size_t partial_bytes, float* out, void* stream) {
+                        int heads, int kv_heads, int head_dim, int max_seq, const int64_t* start_device,
+                        int64_t start, const uint8_t* tree_mask, float scale, float* partial, size_t partial_bytes,
+                        float* out, void* stream) {
   g_last_error[0] = '\0';
   if (n < 1 || n > 64) return set_error(LBK_ERR_ARG, "n must be in [1, 64], got %d", n);
   if (heads < 1 || kv_heads < 1 || heads % kv_heads != 0)
     return set_error(LBK_ERR_ARG, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv_heads);
   if (head_dim != 64 && head_dim != 128) return set_error(LBK_ERR_ARG, "head_dim must be 64 or 128, got %d", head_dim);
   if (max_seq < 1 || max_seq > (1 << 24)) return set_error(LBK_ERR_ARG, "max_seq out of range: %d", max_seq);
-  if (start < 0 || start + n > max_seq)
+  if (n > max_seq) return set_error(LBK_ERR_ARG, "n (%d) exceeds max_seq (%d)", n, max_seq);
+  if (!start_device && (start < 0 || start + n > max_seq))
     return set_error(LBK_ERR_ARG, "positions %lld .. %lld outside [0, %d)", (long long)start, (long long)(start + n - 1),
                      max_seq);
+  // a device start is read at run time: size the grid for the largest one
+  const int64_t sgrid = start_device ? max_seq - n : start;
   if (!q || !k || !v || !k_cache || !v_cache || !out || !partial) return set_error(LBK_ERR_ARG, "NULL pointer");
   for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
                           static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
     if (!aligned16(ptr)) return set_error(LBK_ERR_ARG, "q, k, v and the caches must be 16-byte aligned");
-  const size_t need = lbk_attention_batch_partial_bytes(heads, n, start, head_dim);
+  const size_t need = lbk_attention_batch_partial_bytes(heads, n, sgrid, head_dim);
   if (partial_bytes < need)
     return set_error(LBK_ERR_WORKSPACE, "partial buffer of %zu bytes needed, %zu given", need, partial_bytes);
   AttnBatchParams p;
@@ -2603,14 +2616,15 @@ int lbk_attention_batch(const float* q, const float* k, const float* v, float* k
   p.tree = tree_mask;
   p.part = partial;
   p.out = out;
+  p.start_ptr = start_device;
   p.start = start;
   p.N = n;
   p.heads = heads;
   p.kvh = kv_heads;
   p.rep = heads / kv_heads;
   p.max_seq = max_seq;
-  p.ch = attn_batch_ch(heads, n, start);
-  p.chunks = int(ceil_div(start + n, p.ch));
+  p.ch = attn_batch_ch(heads, n, sgrid);
+  p.chunks = int(ceil_div(sgrid + n, p.ch));
   p.qt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
   p.ps = 4 / p.qt;
   p.scale = scale;

@@ -219,13 +219,16 @@ class LittleBitDecoder:
         _lib.check(rc, "lbk_attention_decode")
         return out
 
-    def _attention_batch_hip(self, q, k, v, kc, vc, start: int, tree_mask: Optional[torch.Tensor]):
-        """N new tokens in one launch pair (causal or ``tree_mask``)."""
+    def _attention_batch_hip(self, q, k, v, kc, vc, start: int, tree_mask: Optional[torch.Tensor],
+                             pos_t: Optional[torch.Tensor] = None):
+        """N new tokens in one launch pair (causal or ``tree_mask``); with
+        ``pos_t`` the start is read on the device (graph-capturable)."""
         from . import _lib
         c = self.config
         N = q.shape[0]
         lib = _lib.load()
-        need = int(lib.lbk_attention_batch_partial_bytes(c.num_attention_heads, N, int(start), c.head_dim))
+        grid_start = self.max_seq_len - N if pos_t is not None else int(start)
+        need = int(lib.lbk_attention_batch_partial_bytes(c.num_attention_heads, N, grid_start, c.head_dim))
         if self._batch_part is None or self._batch_part.numel() * 4 < need:
             self._batch_part = torch.empty(max(need // 4, 1), dtype=torch.float32, device=q.device)
         out = torch.empty((N, c.num_attention_heads * c.head_dim), dtype=torch.float32, device=q.device)
@@ -235,7 +238,8 @@ class LittleBitDecoder:
             tm = tree_mask.to(device=q.device, dtype=torch.uint8).contiguous()
         rc = lib.lbk_attention_batch(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), N, c.num_attention_heads,
-            c.num_key_value_heads, c.head_dim, self.max_seq_len, int(start), None if tm is None else tm.data_ptr(),
+            c.num_key_value_heads, c.head_dim, self.max_seq_len, None if pos_t is None else pos_t.data_ptr(),
+            int(start), None if tm is None else tm.data_ptr(),
             float(c.attn_scale), self._batch_part.data_ptr(), self._batch_part.numel() * 4, out.data_ptr(),
             torch.cuda.current_stream(q.device).cuda_stream)
         _lib.check(rc, "lbk_attention_batch")

@@ -177,7 +177,7 @@ def test_attention_batch_kernel(gpu, n, heads, kvh, hd, max_seq, start, tree):
     old_k = kc.clone()
     print(f"[attention_batch] n={n} heads={heads} kvh={kvh} hd={hd} start={start} tree={tree}", flush=True)
     rc = lib.lbk_attention_batch(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), n, heads,
-                                 kvh, hd, max_seq, start, None if tm is None else tm.data_ptr(), scale, part.data_ptr(),
+                                 kvh, hd, max_seq, None, start, None if tm is None else tm.data_ptr(), scale, part.data_ptr(),
                                  part.numel() * 4, out.data_ptr(), None)
     L.check(rc, "lbk_attention_batch")
     torch.cuda.synchronize()
@@ -189,18 +189,56 @@ def test_attention_batch_kernel(gpu, n, heads, kvh, hd, max_seq, start, tree):
     assert torch.equal(kc[:, :start], old_k[:, :start]) and torch.equal(kc[:, start + n:], old_k[:, start + n:])
 
 
+@pytest.mark.parametrize("n,tree", [(1, False), (8, False), (5, True)])
+def test_attention_batch_device_start(gpu, n, tree):
+    """A start read from device memory (the host value ignored) gives the
+    host-start result and cache; a start whose positions leave the cache
+    stores nothing and yields zeros."""
+    import littlebit_amd._lib as L
+    heads, kvh, hd, max_seq, start = 8, 2, 128, 300, 211
+    g = torch.Generator(device="cpu").manual_seed(7 + n)
+    kc0 = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    vc0 = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    q, k, v = (torch.randn((n, w * hd), generator=g).to(gpu) for w in (heads, kvh, kvh))
+    tm = (torch.rand((n, n), generator=g) < 0.5) | torch.eye(n, dtype=torch.bool)
+    tm = tm.to(torch.uint8).to(gpu) if tree else None
+    lib = L.load()
+    part = torch.empty(lib.lbk_attention_batch_partial_bytes(heads, n, max_seq - n, hd) // 4 + 1, device=gpu)
+
+    def run(dev_start, host_start):
+        kc, vc = kc0.clone(), vc0.clone()
+        out = torch.full((n, heads * hd), float("nan"), device=gpu)
+        ds = None if dev_start is None else torch.tensor([dev_start], dtype=torch.int64, device=gpu)
+        print(f"[attention_batch_dev] n={n} tree={tree} dev={dev_start} host={host_start}", flush=True)
+        rc = lib.lbk_attention_batch(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), n,
+                                     heads, kvh, hd, max_seq, None if ds is None else ds.data_ptr(), host_start,
+                                     None if tm is None else tm.data_ptr(), hd ** -0.5, part.data_ptr(),
+                                     part.numel() * 4, out.data_ptr(), None)
+        L.check(rc, "lbk_attention_batch")
+        torch.cuda.synchronize()
+        return out, kc, vc
+
+    ref, kr, vr = run(None, start)
+    out, kd, vd = run(start, 0)
+    assert O.rel_err(out.cpu().numpy(), ref.cpu().numpy()) <= 1e-6
+    assert torch.equal(kd, kr) and torch.equal(vd, vr)
+    out, kd, vd = run(max_seq - n + 1, 0)  # last position past the cache
+    assert torch.equal(out, torch.zeros_like(out))
+    assert torch.equal(kd, kc0) and torch.equal(vd, vc0)
+
+
 def test_attention_batch_rejects_bad_args(gpu):
     import littlebit_amd._lib as L
     lib = L.load()
     x = torch.zeros(1 << 16, device=gpu)
     p = x.data_ptr()
     big = x.numel() * 4
-    assert lib.lbk_attention_batch(p, p, p, p, p, 65, 4, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
-    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 6, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
-    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 96, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
-    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, 121, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
-    assert lib.lbk_attention_batch(p + 4, p, p, p, p, 8, 4, 4, 64, 128, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
-    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, 0, None, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
+    assert lib.lbk_attention_batch(p, p, p, p, p, 65, 4, 4, 64, 128, None, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 6, 4, 64, 128, None, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 96, 128, None, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, None, 121, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p + 4, p, p, p, p, 8, 4, 4, 64, 128, None, 0, None, 1.0, p, big, p, None) == L.LBK_ERR_ARG
+    assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, None, 0, None, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
 
 
 def test_batch_equals_token_by_token(gpu):
