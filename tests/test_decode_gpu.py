@@ -99,35 +99,41 @@ def test_decoder_matches_float64_reference(gpu, residual, fuse):
 @pytest.mark.parametrize("device_pos", [False, True])
 def test_attention_decode_kernel(gpu, heads, kvh, hd, max_seq, pos, device_pos):
     """lbk_attention_decode against torch: softmax(scale q.K) V over 0..pos,
-    the new k/v used at pos and stored into the cache."""
+    the new k/v used at pos and stored into the cache.  Two calls share one
+    scratch, the second at an earlier position (fewer chunks)."""
     import littlebit_amd._lib as L
-    g = torch.Generator(device="cpu").manual_seed(pos + heads)
-    kc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
-    vc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
-    q = torch.randn((heads * hd,), generator=g).to(gpu)
-    k = torch.randn((kvh * hd,), generator=g).to(gpu)
-    v = torch.randn((kvh * hd,), generator=g).to(gpu)
-    scale = hd ** -0.5
-    K = kc.clone()
-    V = vc.clone()
-    K[:, pos] = k.view(kvh, hd)
-    V[:, pos] = v.view(kvh, hd)
-    rep = heads // kvh
-    qg = q.view(kvh, rep, hd).double().cpu()
-    s = torch.einsum("grd,gtd->grt", qg, K[:, :pos + 1].double().cpu()) * scale
-    ref = torch.einsum("grt,gtd->grd", torch.softmax(s, dim=-1), V[:, :pos + 1].double().cpu()).reshape(-1)
     lib = L.load()
-    part = torch.empty(lib.lbk_attention_partial_bytes(heads, max_seq, hd) // 4 + 1, device=gpu)
-    out = torch.full((heads * hd,), float("nan"), device=gpu)
-    pos_t = torch.tensor([pos], dtype=torch.int64, device=gpu)
-    rc = lib.lbk_attention_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads, kvh,
-                                  hd, max_seq, pos_t.data_ptr() if device_pos else None, 0 if device_pos else pos,
-                                  scale, part.data_ptr(), part.numel() * 4, out.data_ptr(), None)
-    L.check(rc, "lbk_attention_decode")
-    torch.cuda.synchronize()
-    assert O.rel_err(out.cpu().numpy(), ref.numpy()) <= 1e-5
-    assert torch.equal(kc[:, pos], k.view(kvh, hd)) and torch.equal(vc[:, pos], v.view(kvh, hd))
-    assert torch.equal(kc[:, :pos], K[:, :pos])  # nothing else changed
+    need = lib.lbk_attention_partial_bytes(heads, max_seq, hd)
+    part = torch.empty(need // 4 + 1, device=gpu)
+    for call, at in enumerate((pos, pos // 2)):
+        g = torch.Generator(device="cpu").manual_seed(at + heads + 17 * call)
+        kc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+        vc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+        q = torch.randn((heads * hd,), generator=g).to(gpu)
+        k = torch.randn((kvh * hd,), generator=g).to(gpu)
+        v = torch.randn((kvh * hd,), generator=g).to(gpu)
+        scale = hd ** -0.5
+        K = kc.clone()
+        V = vc.clone()
+        K[:, at] = k.view(kvh, hd)
+        V[:, at] = v.view(kvh, hd)
+        rep = heads // kvh
+        qg = q.view(kvh, rep, hd).double().cpu()
+        s = torch.einsum("grd,gtd->grt", qg, K[:, :at + 1].double().cpu()) * scale
+        ref = torch.einsum("grt,gtd->grd", torch.softmax(s, dim=-1), V[:, :at + 1].double().cpu()).reshape(-1)
+        out = torch.full((heads * hd,), float("nan"), device=gpu)
+        pos_t = torch.tensor([at], dtype=torch.int64, device=gpu)
+        print(f"[attention_decode] heads={heads} kvh={kvh} hd={hd} max_seq={max_seq} pos={at} dev={device_pos}",
+              flush=True)
+        rc = lib.lbk_attention_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads,
+                                      kvh, hd, max_seq, pos_t.data_ptr() if device_pos else None,
+                                      0 if device_pos else at, scale, part.data_ptr(), part.numel() * 4,
+                                      out.data_ptr(), None)
+        L.check(rc, "lbk_attention_decode")
+        torch.cuda.synchronize()
+        assert O.rel_err(out.cpu().numpy(), ref.numpy()) <= 1e-5
+        assert torch.equal(kc[:, at], k.view(kvh, hd)) and torch.equal(vc[:, at], v.view(kvh, hd))
+        assert torch.equal(kc[:, :at], K[:, :at])  # nothing else changed
 
 
 def test_attention_decode_rejects_bad_args(gpu):
