@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 4
+#define LBK_ABI_VERSION 5
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -76,15 +76,31 @@ typedef struct lbk_projection {
  * applies these inline, patches/littlebit_cpu_optimized.cpp:1370-1438):
  *   LBK_INPUT_PLAIN     x
  *   LBK_INPUT_RMSNORM   x[m, k] / sqrt(mean_k x[m, k]^2 + rms_eps) * rms_weight[k]
- *   LBK_INPUT_SILU_MUL  x[m, k] / (1 + exp(-x[m, k])) * x1[m, k]  (x = gate, x1 = up) */
+ *   LBK_INPUT_SILU_MUL  x[m, k] / (1 + exp(-x[m, k])) * x1[m, k]  (x = gate, x1 = up)
+ *   LBK_INPUT_ATTN_MERGE  the output of one token's attention, merged from
+ *                       the per-chunk partials that lbk_attention_decode
+ *                       leaves when called with out = NULL: x = those
+ *                       partials (fp32, 16-byte aligned), M = 1,
+ *                       K = heads * head_dim, with that call's head_dim,
+ *                       max_seq and position (pos_device when not NULL, else
+ *                       pos); a position outside [0, max_seq) reads as zeros.
+ *                       The o projection of the decode step then needs no
+ *                       separate merge launch (fused_attention_inline feeding
+ *                       o_proj, patches/littlebit_cpu_optimized.cpp:1441-1510,
+ *                       1736-1750). */
 #define LBK_INPUT_PLAIN 0
 #define LBK_INPUT_RMSNORM 1
 #define LBK_INPUT_SILU_MUL 2
+#define LBK_INPUT_ATTN_MERGE 3
 typedef struct lbk_input {
   int kind;
-  const float* rms_weight; /* [K] fp32 (RMSNORM) */
+  const float* rms_weight;   /* [K] fp32 (RMSNORM) */
   float rms_eps;
-  const void* x1;          /* [M, K] of x_dtype (SILU_MUL) */
+  const void* x1;            /* [M, K] of x_dtype (SILU_MUL) */
+  int head_dim;              /* ATTN_MERGE: 64 or 128 */
+  int max_seq;               /* ATTN_MERGE */
+  const int64_t* pos_device; /* ATTN_MERGE: position on the device, or NULL */
+  int64_t pos;               /* ATTN_MERGE: position when pos_device is NULL */
 } lbk_input;
 
 #define LBK_MAX_GROUP 4
@@ -154,8 +170,10 @@ int lbk_littlebit_linear(const float* input, int64_t M, const float* v2,
  * stored into k_cache / v_cache [kv_heads][max_seq][head_dim].  pos is read
  * from pos_device when it is not NULL (so a captured graph follows a
  * position the device advances), else taken from pos.  partial: scratch of
- * lbk_attention_partial_bytes() (needed when max_seq > 32).  A position
- * outside [0, max_seq) stores nothing and yields zeros.
+ * lbk_attention_partial_bytes() (needed when max_seq > 16 or out is NULL).
+ * A position outside [0, max_seq) stores nothing and yields zeros.  With
+ * out = NULL the call stops at the per-chunk partials (partial 16-byte
+ * aligned), which a projection reads with LBK_INPUT_ATTN_MERGE.
  * Replaces fused_attention_inline (patches/littlebit_cpu_optimized.cpp:
  * 1441-1510) and the per-token attention of cpu_draft_model.py:371-383. */
 size_t lbk_attention_partial_bytes(int heads, int max_seq, int head_dim);

@@ -68,12 +68,17 @@ class LbkInput(ctypes.Structure):
         ("rms_weight", ctypes.c_void_p),
         ("rms_eps", ctypes.c_float),
         ("x1", ctypes.c_void_p),
+        ("head_dim", ctypes.c_int),
+        ("max_seq", ctypes.c_int),
+        ("pos_device", ctypes.c_void_p),
+        ("pos", ctypes.c_int64),
     ]
 
 
 LBK_INPUT_PLAIN = 0
 LBK_INPUT_RMSNORM = 1
 LBK_INPUT_SILU_MUL = 2
+LBK_INPUT_ATTN_MERGE = 3
 LBK_MAX_GROUP = 4
 
 # name -> (restype, argtypes); must list every function of include/littlebit_amd.h

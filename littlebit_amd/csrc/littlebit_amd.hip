@@ -144,6 +144,11 @@ struct Raw8<uint16_t> {
 // MFMA path parameters
 // ---------------------------------------------------------------------------
 constexpr int kMaxWaveSteps = 32;  // rank steps (both branches) per expand wave
+// positions per block of the decode attention: more, smaller blocks measured
+// faster at KV 512 than 32 or 64; its partials are rows of kAttnPad + head_dim
+// floats (o, then max and exp-sum, 16-byte aligned rows)
+constexpr int kAttnChunk = 16;
+constexpr int kAttnPad = 4;
 constexpr int kMaxProj = 4;        // projections sharing one input in a group call
 constexpr int kMaxSeg = 2 * kMaxProj;
 // floats per latent half: M <= 16 rows of the padded ranks of every branch
@@ -195,6 +200,11 @@ struct MfmaParams {
   const void* x1;       // second input of LBK_INPUT_SILU_MUL
   const float* nw;      // RMSNorm weight [K]
   float eps;            // RMSNorm epsilon
+  // LBK_INPUT_ATTN_MERGE: x = attention partials [K / ahd][achunks][ahd + 4];
+  // position from apos when set, else apos_host
+  const int64_t* apos;
+  int64_t apos_host;
+  int ahd, achunks, amax_seq;
   float* t2;       // two halves of kTHalf floats; per segment [M][RP] latent, l-scaled,
                    // then kMaxMfmaM floats: per row the sum of x^2 (RMSNorm input)
   uint32_t* sync;  // [0] P: half the next latent kernel accumulates into
@@ -517,6 +527,112 @@ __device__ __forceinline__ void stage_latent_rows(const MfmaParams& p, const flo
   }
 }
 
+// LBK_INPUT_ATTN_MERGE, one row: the block's KC = 8 * NCH columns of the
+// attention output, merged from the decode attention's per-chunk partials
+// (o[hd], m, l of the positions of chunk j; chunks j <= pos / kAttnChunk):
+//   x[k] = sum_j exp(m_j - M) o_j[k % hd] / sum_j exp(m_j - M) l_j,  M = max_j m_j
+// for head k / hd (the merge of attn_combine_kernel, done by the consumer so
+// that the draft step has no merge launch).  Wave w takes chunks w, w + 4, ..
+// in rounds of JB whose loads issue together, lane DPL consecutive columns
+// (one head); the waves' (max, num, den) are merged through LDS.  A position
+// outside [0, max_seq) gives x = 0 (the attention yields zeros there).
+template <int NCH>
+__device__ __forceinline__ void stage_latent_attn(const MfmaParams& p, const float* __restrict__ g, int k0,
+                                                  u32x4* lds, int tid) {
+  constexpr int KC = 8 * NCH, DPL = KC / 64, JB = DPL <= 4 ? 12 : DPL == 8 ? 8 : 4;
+  static_assert(DPL == 2 || DPL == 4 || DPL == 8 || DPL == 16, "columns per lane");
+  __shared__ float w_m[4][64], w_d[4][64];
+  __shared__ float w_n[4][KC];
+  __shared__ float xs[KC];
+  const int wave = tid >> 6, lane = tid & 63;
+  // this thread's g chunk (threads c < NCH), loaded before anything waits
+  Raw8<float> gr;
+  const bool gvalid = tid < NCH && k0 + 8 * tid < p.K;
+  if (gvalid) gr.load(g + k0 + 8 * tid);
+  const int64_t pos = p.apos ? *p.apos : p.apos_host;
+  const int used = (pos >= 0 && pos < p.amax_seq) ? int(pos / kAttnChunk) + 1 : 0;
+  const int hd = p.ahd, stride = hd + kAttnPad;
+  const int kcol = k0 + lane * DPL;
+  const bool cvalid = kcol < p.K;  // DPL divides hd: a lane's columns are wholly inside K or past it
+  const int head = cvalid ? kcol / hd : 0;
+  const int d = kcol - head * hd;
+  const float* __restrict__ ph = static_cast<const float*>(p.x) + size_t(head) * p.achunks * stride;
+  float M = -INFINITY, den = 0.f, num[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) num[i] = 0.f;
+  for (int j0 = wave; j0 < used; j0 += 4 * JB) {
+    float2 ml[JB];
+    float ov[JB][DPL];
+#pragma unroll
+    for (int b = 0; b < JB; ++b) {
+      const float* row = ph + size_t(min(j0 + 4 * b, used - 1)) * stride;
+      ml[b] = *reinterpret_cast<const float2*>(row + hd);
+      if constexpr (DPL == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(row + d);
+        ov[b][0] = v.x;
+        ov[b][1] = v.y;
+      } else {
+#pragma unroll
+        for (int q = 0; q < DPL / 4; ++q) {
+          const float4 v = *reinterpret_cast<const float4*>(row + d + 4 * q);
+          ov[b][4 * q] = v.x;
+          ov[b][4 * q + 1] = v.y;
+          ov[b][4 * q + 2] = v.z;
+          ov[b][4 * q + 3] = v.w;
+        }
+      }
+    }
+    float bm = M;
+#pragma unroll
+    for (int b = 0; b < JB; ++b)
+      if (j0 + 4 * b < used) bm = fmaxf(bm, ml[b].x);
+    const float cs = M == -INFINITY ? 0.f : __expf(M - bm);  // bm is finite: chunk j0 < used
+    den *= cs;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) num[i] *= cs;
+#pragma unroll
+    for (int b = 0; b < JB; ++b) {
+      const float w = j0 + 4 * b < used ? __expf(ml[b].x - bm) : 0.f;
+      den += w * ml[b].y;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) num[i] += w * ov[b][i];
+    }
+    M = bm;
+  }
+  w_m[wave][lane] = M;
+  w_d[wave][lane] = den;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) w_n[wave][lane * DPL + i] = num[i];
+  __syncthreads();
+  for (int k = tid; k < KC; k += kBlock) {
+    const int ln = k / DPL;
+    float mx = fmaxf(fmaxf(w_m[0][ln], w_m[1][ln]), fmaxf(w_m[2][ln], w_m[3][ln]));
+    float nn = 0.f, dd = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = w_m[w][ln] == -INFINITY ? 0.f : __expf(w_m[w][ln] - mx);
+      nn += e * w_n[w][k];
+      dd += e * w_d[w][ln];
+    }
+    xs[k] = (mx == -INFINITY || k0 + k >= p.K) ? 0.f : nn / dd;
+  }
+  __syncthreads();
+  if (tid < NCH) {
+    u32x4 hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+    if (gvalid) {
+      float a[8], gv[8];
+      gr.get(gv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = xs[8 * tid + e] * gv[e];
+      split8(a, hi, lo);
+    }
+    u32x4* base = lds + size_t(tid) * Compact<1>::ROWS;
+    base[0] = hi;
+    base[Compact<1>::MR] = lo;
+    base[2 * Compact<1>::MR] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Stage 1 (MFMA): t += l * (V_sign . (g*x)) over this block's k-chunk
 // grid.x = (row-blocks of all segments) * nkc, block = 256 threads (4 waves)
@@ -606,7 +722,9 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
     // first row-block add their chunk's sums of squares next to t, and the
     // expand kernel scales t by 1/rms when it stages it
     float* ssq_out = p.t2 + size_t(h) * kTHalf + p.tsize;
-    if (p.xmode == LBK_INPUT_RMSNORM)
+    if (MT == 1 && p.xmode == LBK_INPUT_ATTN_MERGE) {
+      if constexpr (MT == 1) stage_latent_attn<NCH>(p, g, k0, lds_a, tid);
+    } else if (p.xmode == LBK_INPUT_RMSNORM)
       stage_latent_rows<XT, MT, NCH, LBK_INPUT_RMSNORM>(p, g, k0, lds_a, tid, rbk == 0, ssq_out);
     else if (p.xmode == LBK_INPUT_SILU_MUL)
       stage_latent_rows<XT, MT, NCH, LBK_INPUT_SILU_MUL>(p, g, k0, lds_a, tid, false, ssq_out);
@@ -1479,7 +1597,6 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
 // attn_combine_kernel merges.  pos is read on the device when pos_ptr is set (graph replay);
 // pos >= max_seq writes nothing but zeros to out.
 // ---------------------------------------------------------------------------
-constexpr int kAttnChunk = 16;  // positions per block: more, smaller blocks measured faster at KV 512 than 32 or 64
 constexpr int kAttnThreads = 256;
 
 struct AttnParams {
@@ -1492,8 +1609,8 @@ struct AttnParams {
   int64_t pos;
   int heads, rep, max_seq, chunks;
   float scale;
-  float* part;           // [heads][chunks][HD + 2]
-  float* out;            // [heads * HD]
+  float* part;           // [heads][chunks][HD + kAttnPad]: o, max, exp-sum
+  float* out;            // [heads * HD]; null: the partials are the result (a consumer merges them)
 };
 
 __device__ __forceinline__ int64_t attn_pos(const AttnParams& p) { return p.pos_ptr ? *p.pos_ptr : p.pos; }
@@ -1509,9 +1626,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
   const int wave = tid >> 6, lane = tid & 63;
   const int kv = h / p.rep;
   const int64_t pos = attn_pos(p);
-  float* part = p.part + (size_t(h) * p.chunks + c) * (HD + 2);
+  float* part = p.part + (size_t(h) * p.chunks + c) * (HD + kAttnPad);
   if (pos < 0 || pos >= p.max_seq) {  // out of range: nothing is read or stored
-    if (c == 0 && tid < HD) p.out[size_t(h) * HD + tid] = 0.f;
+    if (p.out && c == 0 && tid < HD) p.out[size_t(h) * HD + tid] = 0.f;
     return;
   }
   const int S = int(pos) + 1;
@@ -1639,7 +1756,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
     float od = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) od += ored[w][tid];
-    if (p.chunks == 1) {
+    if (p.chunks == 1 && p.out) {
       p.out[size_t(h) * HD + tid] = od / sm;
     } else {
       part[tid] = od;
@@ -1659,15 +1776,15 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
   const int h = int(blockIdx.x), d = int(threadIdx.x);
   const int64_t pos = attn_pos(p);
   if (pos < 0 || pos >= p.max_seq) return;  // out was zeroed by attn_decode_kernel
-  const float* part = p.part + size_t(h) * p.chunks * (HD + 2);
+  const float* part = p.part + size_t(h) * p.chunks * (HD + kAttnPad);
   const int used = int(pos / kAttnChunk) + 1;  // chunks past pos hold empty partials
   float M = -INFINITY;
 #pragma unroll 8
-  for (int c = 0; c < used; ++c) M = fmaxf(M, part[size_t(c) * (HD + 2) + HD]);
+  for (int c = 0; c < used; ++c) M = fmaxf(M, part[size_t(c) * (HD + kAttnPad) + HD]);
   float num = 0.f, den = 0.f;
 #pragma unroll 8
   for (int c = 0; c < used; ++c) {
-    const float* pc = part + size_t(c) * (HD + 2);
+    const float* pc = part + size_t(c) * (HD + kAttnPad);
     const float w = __expf(pc[HD] - M);  // chunk 0 holds position 0, so M is finite
     num += pc[d] * w;
     den += pc[HD + 1] * w;
@@ -1947,6 +2064,9 @@ struct InputDesc {
   const float* nw;
   float eps;
   const void* x1;
+  int head_dim, max_seq;      // LBK_INPUT_ATTN_MERGE
+  const int64_t* pos_device;
+  int64_t pos;
 };
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
@@ -2234,6 +2354,11 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.x1 = in.x1;
   p.nw = in.nw;
   p.eps = in.eps;
+  p.apos = in.pos_device;
+  p.apos_host = in.pos;
+  p.ahd = in.head_dim;
+  p.amax_seq = in.max_seq;
+  p.achunks = in.kind == LBK_INPUT_ATTN_MERGE ? int(ceil_div(in.max_seq, kAttnChunk)) : 0;
   bool xvec = (K % 8) == 0 && aligned16(x) && (!in.x1 || aligned16(in.x1)) && (!in.nw || aligned16(in.nw));
   bool wvec = true;
   int rb = 0, tbase = 0, si = 0, tile = 0;
@@ -2277,6 +2402,8 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.wvec = wvec && p.KW % std::max(pl.wpl, 4) == 0 ? 1 : 0;
   p.xvec = xvec ? 1 : 0;
   p.late_rs = xvec && in.kind == LBK_INPUT_RMSNORM ? 1 : 0;
+  if (in.kind == LBK_INPUT_ATTN_MERGE && (!xvec || M != 1))
+    return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE needs one row and 16-byte aligned g of every branch");
   char* ws = static_cast<char*>(workspace);
   p.sync = reinterpret_cast<uint32_t*>(ws);
   p.t2 = reinterpret_cast<float*>(ws + kTOffset);
@@ -2374,10 +2501,27 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
                   const lbk_input* input, int y_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = validate_group(pd, np, M, K);
   if (rc != LBK_OK) return rc;
-  InputDesc in{LBK_INPUT_PLAIN, nullptr, 0.f, nullptr};
+  InputDesc in{LBK_INPUT_PLAIN, nullptr, 0.f, nullptr, 0, 0, nullptr, 0};
   if (input) {
-    in = InputDesc{input->kind, input->rms_weight, input->rms_eps, input->x1};
-    if (in.kind == LBK_INPUT_RMSNORM) {
+    in = InputDesc{input->kind, input->rms_weight, input->rms_eps, input->x1,
+                   0, 0, nullptr, 0};
+    if (in.kind == LBK_INPUT_ATTN_MERGE) {
+      in.nw = nullptr;
+      in.x1 = nullptr;
+      in.head_dim = input->head_dim;
+      in.max_seq = input->max_seq;
+      in.pos_device = input->pos_device;
+      in.pos = input->pos;
+      if (M != 1 && M != 0) return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE needs M == 1, got %lld", (long long)M);
+      if (x_dtype != LBK_F32) return set_error(LBK_ERR_DTYPE, "LBK_INPUT_ATTN_MERGE reads fp32 partials");
+      if (in.head_dim != 64 && in.head_dim != 128)
+        return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: head_dim must be 64 or 128, got %d", in.head_dim);
+      if (K % in.head_dim != 0)
+        return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: K (%lld) must be heads * head_dim", (long long)K);
+      if (in.max_seq < 1 || in.max_seq > (1 << 24))
+        return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: max_seq out of range: %d", in.max_seq);
+      if (x && !aligned16(x)) return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: partials must be 16-byte aligned");
+    } else if (in.kind == LBK_INPUT_RMSNORM) {
       if (!in.nw) return set_error(LBK_ERR_ARG, "LBK_INPUT_RMSNORM needs rms_weight");
       if (!(in.eps >= 0.f)) return set_error(LBK_ERR_ARG, "rms_eps must be >= 0");
       in.x1 = nullptr;
@@ -2398,6 +2542,8 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
   for (int q = 0; q < np; ++q)
     if (!pd[q].y) return set_error(LBK_ERR_ARG, "projection %d: y is NULL", q);
   const Plan pl = make_plan(pd, np, M, K);
+  if (in.kind == LBK_INPUT_ATTN_MERGE && (!pl.mfma || pl.chunk > 0))
+    return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: the projections have no one-row decode plan");
   if (!workspace || workspace_bytes < pl.ws_total)
     return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_total, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2520,7 +2666,7 @@ int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols, int32_t* out
 size_t lbk_attention_partial_bytes(int heads, int max_seq, int head_dim) {
   if (heads < 1 || max_seq < 1 || head_dim < 1) return 0;
   const int64_t chunks = ceil_div(max_seq, kAttnChunk);
-  return size_t(heads) * size_t(chunks) * size_t(head_dim + 2) * sizeof(float);
+  return size_t(heads) * size_t(chunks) * size_t(head_dim + kAttnPad) * sizeof(float);
 }
 
 int lbk_attention_decode(const float* q, const float* k, const float* v, float* k_cache, float* v_cache, int heads,
@@ -2533,14 +2679,16 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   if (max_seq < 1 || max_seq > (1 << 24)) return set_error(LBK_ERR_ARG, "max_seq out of range: %d", max_seq);
   if (!pos_device && (pos < 0 || pos >= max_seq))
     return set_error(LBK_ERR_ARG, "pos %lld outside [0, %d)", (long long)pos, max_seq);
-  if (!q || !k || !v || !k_cache || !v_cache || !out) return set_error(LBK_ERR_ARG, "NULL pointer");
+  if (!q || !k || !v || !k_cache || !v_cache) return set_error(LBK_ERR_ARG, "NULL pointer");
   for (const void* ptr : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
                           static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
     if (!aligned16(ptr)) return set_error(LBK_ERR_ARG, "q, k, v and the caches must be 16-byte aligned");
   const int chunks = int(ceil_div(max_seq, kAttnChunk));
   const size_t need = lbk_attention_partial_bytes(heads, max_seq, head_dim);
-  if (chunks > 1 && (!partial || partial_bytes < need))
+  if ((chunks > 1 || !out) && (!partial || partial_bytes < need))
     return set_error(LBK_ERR_WORKSPACE, "partial buffer of %zu bytes needed, %zu given", need, partial_bytes);
+  if (!out && !aligned16(partial))
+    return set_error(LBK_ERR_ARG, "partials for a consumer (out NULL) must be 16-byte aligned");
   AttnParams p;
   p.q = q;
   p.k = k;
@@ -2561,7 +2709,7 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   if (head_dim == 128) hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kAttnThreads), 0, s, p);
   else hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kAttnThreads), 0, s, p);
   int rc = check_launch("attn_decode_kernel");
-  if (rc != LBK_OK || chunks == 1) return rc;
+  if (rc != LBK_OK || chunks == 1 || !out) return rc;
   if (head_dim == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(heads), dim3(128), 0, s, p);
   else hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(heads), dim3(64), 0, s, p);
   return check_launch("attn_combine_kernel");

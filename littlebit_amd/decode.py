@@ -219,6 +219,21 @@ class LittleBitDecoder:
         _lib.check(rc, "lbk_attention_decode")
         return out
 
+    def _attention_partials(self, li: int, q, k, v, start: int, pos_t: Optional[torch.Tensor]):
+        """One token's attention stopped at its per-chunk partials, for the
+        o projection to merge (``lbk_attention_decode`` without an output)."""
+        from . import _lib
+        from .ops import AttentionPartials
+        c = self.config
+        q, k, v = (t.to(torch.float32).contiguous() for t in (q, k, v))
+        rc = _lib.load().lbk_attention_decode(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[li].data_ptr(), self.v_cache[li].data_ptr(),
+            c.num_attention_heads, c.num_key_value_heads, c.head_dim, self.max_seq_len,
+            None if pos_t is None else pos_t.data_ptr(), int(start), float(c.attn_scale), self._attn_part.data_ptr(),
+            self._attn_part.numel() * 4, None, torch.cuda.current_stream(q.device).cuda_stream)
+        _lib.check(rc, "lbk_attention_decode")
+        return AttentionPartials(self._attn_part, c.head_dim, self.max_seq_len, pos_t, int(start))
+
     def _attention_batch_hip(self, q, k, v, kc, vc, start: int, tree_mask: Optional[torch.Tensor],
                              pos_t: Optional[torch.Tensor] = None):
         """N new tokens in one launch pair (causal or ``tree_mask``); with
@@ -265,10 +280,14 @@ class LittleBitDecoder:
         # the norms, SiLU * up and the residual adds run inside the projection
         # calls; x (a private copy) is updated in place by o and down
         x = x.to(torch.float32).clone()
+        merge = x.shape[0] == 1 and tree_mask is None and self._hip_attn
         for li, L in enumerate(self.layers):
             q, k, v = L["qkv"].forward(x, rms_weight=L["ln1"], rms_eps=eps)
-            a = self._attention(li, q, k, v, start, length, pos_t, tree_mask)
-            L["o"].forward(a, out=x, residual=x)
+            if merge:  # o reads the attention's per-chunk partials and merges them itself
+                L["o"].forward(None, out=x, residual=x, attn=self._attention_partials(li, q, k, v, start, pos_t))
+            else:
+                a = self._attention(li, q, k, v, start, length, pos_t, tree_mask)
+                L["o"].forward(a, out=x, residual=x)
             g, u = L["gate_up"].forward(x, rms_weight=L["ln2"], rms_eps=eps)
             L["down"].forward(g, out=x, residual=x, x_up=u)
         return rms_norm(x, self.final_norm, eps)

@@ -117,6 +117,19 @@ class LittleBitBranch:
             _check(t.device == dev, f"{name}: all tensors must be on one device")
 
 
+@dataclass
+class AttentionPartials:
+    """The per-chunk partials of one token's attention, as
+    ``lbk_attention_decode`` leaves them when called without an output
+    (fp32 [heads][ceil(max_seq / 16)][head_dim + 4]).  A projection given
+    them as its input merges the attention output while it stages it."""
+    partials: torch.Tensor
+    head_dim: int
+    max_seq: int
+    pos: Optional[torch.Tensor] = None  # int64 [1] on the device (graph replay)
+    pos_host: int = 0                   # the position when ``pos`` is None
+
+
 class LittleBitProjection:
     """A projection's branches (draft, optional residual) and optional bias,
     prepared once so that each forward is one C call."""
@@ -158,17 +171,18 @@ class LittleBitProjection:
             _lib.check(_lib.LBK_ERR_ARG, "lbk_linear_workspace_bytes")
         return int(n)
 
-    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+    def forward(self, x: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
                 out_dtype: Optional[torch.dtype] = None, *, rms_weight: Optional[torch.Tensor] = None,
                 rms_eps: float = 1e-6, x_up: Optional[torch.Tensor] = None,
-                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+                residual: Optional[torch.Tensor] = None,
+                attn: Optional[AttentionPartials] = None) -> torch.Tensor:
         """y[..., N] = sum of branches (+ bias) for x[..., K] (fp32 or bf16);
         the fusions of :meth:`LittleBitProjectionGroup.forward`."""
-        if rms_weight is not None or x_up is not None or residual is not None:
+        if rms_weight is not None or x_up is not None or residual is not None or attn is not None:
             if self._group is None:
                 self._group = LittleBitProjectionGroup([self])
             return self._group.forward(x, None if out is None else [out], out_dtype, rms_weight=rms_weight,
-                                       rms_eps=rms_eps, x_up=x_up, residuals=[residual])[0]
+                                       rms_eps=rms_eps, x_up=x_up, residuals=[residual], attn=attn)[0]
         _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
         _check(x.device == self.device, "input must be on the factors' device")
         _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
@@ -234,10 +248,11 @@ class LittleBitProjectionGroup:
             _lib.check(_lib.LBK_ERR_ARG, "lbk_group_workspace_bytes")
         return int(n)
 
-    def forward(self, x: torch.Tensor, outs: Optional[Sequence[torch.Tensor]] = None,
+    def forward(self, x: Optional[torch.Tensor], outs: Optional[Sequence[torch.Tensor]] = None,
                 out_dtype: Optional[torch.dtype] = None, *, rms_weight: Optional[torch.Tensor] = None,
                 rms_eps: float = 1e-6, x_up: Optional[torch.Tensor] = None,
-                residuals: Optional[Sequence[Optional[torch.Tensor]]] = None) -> list:
+                residuals: Optional[Sequence[Optional[torch.Tensor]]] = None,
+                attn: Optional[AttentionPartials] = None) -> list:
         """Outputs of every projection for input x [..., K].
 
         Fusions (the reference decode step's inline operations,
@@ -245,8 +260,28 @@ class LittleBitProjectionGroup:
           ``rms_weight``  the projections read RMSNorm(x) * rms_weight;
           ``x_up``        they read SiLU(x) * x_up (x the gate output);
           ``residuals``   per projection an fp32 [..., N] tensor added to its
-                          output; it may be the output tensor itself.
+                          output; it may be the output tensor itself;
+          ``attn``        (x None, one row) they read the attention output
+                          merged from ``attn``'s partials (patch:1441-1510
+                          feeding o_proj), outputs [1, N].
         """
+        if attn is not None:
+            _check(x is None and rms_weight is None and x_up is None, "attn replaces x and the other input fusions")
+            part = attn.partials
+            _require_cuda(part, "attn.partials")
+            _check(part.dtype == torch.float32 and part.is_contiguous() and part.device == self.device,
+                   "attn.partials must be a contiguous float32 tensor on the factors' device")
+            if attn.pos is not None:
+                _require_cuda(attn.pos, "attn.pos")
+                _check(attn.pos.dtype == torch.int64, "attn.pos must be int64")
+            odt = out_dtype or torch.float32
+            x = part
+            x2 = part
+            M = 1
+            lead = (1,)
+            inp = _lib.LbkInput(_lib.LBK_INPUT_ATTN_MERGE, None, 0.0, None, int(attn.head_dim), int(attn.max_seq),
+                                None if attn.pos is None else attn.pos.data_ptr(), int(attn.pos_host))
+            return self._launch(x2, M, lead, odt, outs, inp, residuals)
         _check(isinstance(x, torch.Tensor) and x.is_cuda, "input must be a GPU tensor")
         _check(x.device == self.device, "input must be on the factors' device")
         _check(x.dtype in _DTYPE_CODES, f"input dtype {x.dtype} unsupported (float32 or bfloat16)")
@@ -259,18 +294,7 @@ class LittleBitProjectionGroup:
             x2 = x2.contiguous()
         M = x2.shape[0]
         odt = out_dtype or x.dtype
-        _check(odt in _DTYPE_CODES, f"output dtype {odt} unsupported")
-        if outs is None:
-            outs = [torch.empty((*lead, p.out_features), dtype=odt, device=x.device) for p in self.projections]
-        else:
-            _check(len(outs) == len(self.projections), "one output per projection")
-            for o, p in zip(outs, self.projections):
-                _check(o.is_cuda and o.is_contiguous() and o.dtype == odt and o.numel() == M * p.out_features,
-                       "an output has the wrong shape, dtype or layout")
-        if M == 0:
-            return list(outs)
         inp = None
-        keep = []
         if rms_weight is not None:
             _require_cuda(rms_weight, "rms_weight")
             _check(rms_weight.dtype == torch.float32 and rms_weight.numel() == self.in_features,
@@ -280,6 +304,20 @@ class LittleBitProjectionGroup:
             _require_cuda(x_up, "x_up")
             _check(x_up.dtype == x.dtype and x_up.numel() == x.numel(), "x_up must match x in dtype and size")
             inp = _lib.LbkInput(_lib.LBK_INPUT_SILU_MUL, None, 0.0, x_up.data_ptr())
+        return self._launch(x2, M, lead, odt, outs, inp, residuals)
+
+    def _launch(self, x2, M, lead, odt, outs, inp, residuals) -> list:
+        _check(odt in _DTYPE_CODES, f"output dtype {odt} unsupported")
+        if outs is None:
+            outs = [torch.empty((*lead, p.out_features), dtype=odt, device=x2.device) for p in self.projections]
+        else:
+            _check(len(outs) == len(self.projections), "one output per projection")
+            for o, p in zip(outs, self.projections):
+                _check(o.is_cuda and o.is_contiguous() and o.dtype == odt and o.numel() == M * p.out_features,
+                       "an output has the wrong shape, dtype or layout")
+        if M == 0:
+            return list(outs)
+        keep = []
         for i, o in enumerate(outs):
             self._arr[i].y = o.data_ptr()
             r = None if residuals is None else residuals[i]
@@ -289,10 +327,10 @@ class LittleBitProjectionGroup:
                 keep.append(r)
             self._arr[i].residual = None if r is None else r.data_ptr()
         lib = _lib.load()
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        ws = workspace_for(x.device, stream, self.workspace_bytes(M))
+        stream = torch.cuda.current_stream(x2.device).cuda_stream
+        ws = workspace_for(x2.device, stream, self.workspace_bytes(M))
         rc = lib.lbk_group_forward_ex(self._arr, len(self.projections), M, self.in_features, x2.data_ptr(),
-                                      _DTYPE_CODES[x.dtype], ctypes.byref(inp) if inp is not None else None,
+                                      _DTYPE_CODES[x2.dtype], ctypes.byref(inp) if inp is not None else None,
                                       _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
         _lib.check(rc, "lbk_group_forward_ex")
         return list(outs)

@@ -120,8 +120,10 @@ def test_group_struct_layout():
     assert ctypes.sizeof(L.LbkProjection) == 48
     assert L.LbkProjection.out_features.offset == 16 and L.LbkProjection.y.offset == 32
     assert L.LbkProjection.residual.offset == 40
-    assert ctypes.sizeof(L.LbkInput) == 32
+    assert ctypes.sizeof(L.LbkInput) == 56
     assert (L.LbkInput.rms_weight.offset, L.LbkInput.rms_eps.offset, L.LbkInput.x1.offset) == (8, 16, 24)
+    assert (L.LbkInput.head_dim.offset, L.LbkInput.max_seq.offset, L.LbkInput.pos_device.offset,
+            L.LbkInput.pos.offset) == (32, 36, 40, 48)
 
 
 def test_input_kind_validation():
@@ -138,6 +140,19 @@ def test_input_kind_validation():
     silu = L.LbkInput(L.LBK_INPUT_SILU_MUL, None, 0.0, None)
     assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(silu), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
     assert "x1" in L.last_error()
+    # attention partials: one row, fp32, K a multiple of head_dim 64 / 128, aligned
+    att = L.LbkInput(L.LBK_INPUT_ATTN_MERGE, None, 0.0, None, 64, 128, None, 5)
+    assert fx(arr, 2, 2, 64, 0x1000, L.LBK_F32, ctypes.byref(att), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "M == 1" in L.last_error()
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_BF16, ctypes.byref(att), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_DTYPE
+    assert fx(arr, 2, 1, 64, 0x1008, L.LBK_F32, ctypes.byref(att), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "aligned" in L.last_error()
+    att.head_dim = 128
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(att), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "heads * head_dim" in L.last_error()
+    att.head_dim, att.max_seq = 64, 0
+    assert fx(arr, 2, 1, 64, 0x1000, L.LBK_F32, ctypes.byref(att), L.LBK_F32, 0x1000, 1 << 24, None) == L.LBK_ERR_ARG
+    assert "max_seq" in L.last_error()
 
 
 def test_group_validation_errors():

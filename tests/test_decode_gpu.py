@@ -19,15 +19,18 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _cfg():
+def _cfg(hd=32):
+    """4 query / 2 KV heads of hd dims: hd 32 runs the decoder's torch
+    attention, hd 64 its HIP attention (one-token steps with the merge in the
+    o projection, batches with lbk_attention_batch)."""
     from littlebit_amd.decode import DecoderConfig
-    return DecoderConfig(hidden_size=128, intermediate_size=320, num_hidden_layers=2, num_attention_heads=4,
+    return DecoderConfig(hidden_size=4 * hd, intermediate_size=320, num_hidden_layers=2, num_attention_heads=4,
                          num_key_value_heads=2, vocab_size=384, rms_norm_eps=1e-6)
 
 
-def _state(seed, residual=True, draft=(16, 24), res=(40, 56)):
+def _state(seed, residual=True, draft=(16, 24), res=(40, 56), hd=32):
     from littlebit_amd.synthetic import synthetic_runtime_state
-    return synthetic_runtime_state(_cfg(), {"attn": draft[0], "mlp": draft[1]},
+    return synthetic_runtime_state(_cfg(hd), {"attn": draft[0], "mlp": draft[1]},
                                    {"attn": res[0], "mlp": res[1]} if residual else None,
                                    seed=seed, normalized=True)
 
@@ -82,10 +85,11 @@ def ref_hidden(state, cfg, ids, residual):
 
 
 @pytest.mark.parametrize("residual,fuse", [(False, True), (True, True), (True, False)])
-def test_decoder_matches_float64_reference(gpu, residual, fuse):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_decoder_matches_float64_reference(gpu, hd, residual, fuse):
     from littlebit_amd.decode import LittleBitDecoder
-    cfg = _cfg()
-    st = _state(11)
+    cfg = _cfg(hd)
+    st = _state(11, hd=hd)
     dec = LittleBitDecoder(st, cfg, gpu, max_seq_len=64, residual=None if residual else False, fuse=fuse)
     ids = [3, 17, 250, 9, 101, 42, 7]
     h = dec.forward_batch(ids, st["model.embed_tokens.weight"].to(gpu))
@@ -247,24 +251,30 @@ def test_attention_batch_rejects_bad_args(gpu):
     assert lib.lbk_attention_batch(p, p, p, p, p, 8, 4, 4, 64, 128, None, 0, None, 1.0, p, 16, p, None) == L.LBK_ERR_WORKSPACE
 
 
-def test_batch_equals_token_by_token(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_batch_equals_token_by_token(gpu, hd):
     from littlebit_amd.decode import LittleBitDecoder
-    cfg = _cfg()
-    st = _state(12)
+    cfg = _cfg(hd)
+    st = _state(12, hd=hd)
     emb = st["model.embed_tokens.weight"].to(gpu)
     ids = [5, 6, 7, 8, 300, 2]
     a = LittleBitDecoder(st, cfg, gpu, max_seq_len=32)
     b = LittleBitDecoder(st, cfg, gpu, max_seq_len=32)
     hb = a.forward_batch(ids, emb)
     ht = torch.cat([b.forward_token(t, emb) for t in ids])
-    assert O.rel_err(hb.cpu().numpy(), ht.cpu().numpy()) <= 1e-5
+    err = O.rel_err(hb.cpu().numpy(), ht.cpu().numpy())
+    print(f"[batch_vs_tokens] hd={hd} rel_err={err:.2e}", flush=True)
+    # fp32 summation orders differ (batched MFMA attention and row tiles
+    # against one-token steps); a mask or position mistake would be O(1)
+    assert err <= 1e-4
     assert a.cache_pos == b.cache_pos == len(ids)
 
 
-def test_draft_graph_equals_eager_and_rolls_back(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_draft_graph_equals_eager_and_rolls_back(gpu, hd):
     from littlebit_amd.decode import GPUDraftModel
-    cfg = _cfg()
-    st = _state(13, residual=False)
+    cfg = _cfg(hd)
+    st = _state(13, residual=False, hd=hd)
     g = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=True)
     e = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False)
     prompt = torch.tensor([[1, 44, 90, 200, 3]])
@@ -284,10 +294,11 @@ def test_draft_graph_equals_eager_and_rolls_back(gpu):
            [int(t) for t in g.generate_draft_tokens(prompt, draft_length=4)[0]]
 
 
-def test_target_prefix_reuse_and_zero_rows(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_target_prefix_reuse_and_zero_rows(gpu, hd):
     from littlebit_amd.decode import GPUTargetModel
-    cfg = _cfg()
-    d, r = _state(14, residual=False), _state(15, residual=False)
+    cfg = _cfg(hd)
+    d, r = _state(14, residual=False, hd=hd), _state(15, residual=False, hd=hd)
     t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=64)
     fresh = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=64)
     a = torch.tensor([[4, 8, 15, 16, 23]])
@@ -305,10 +316,11 @@ def test_target_prefix_reuse_and_zero_rows(gpu):
     assert O.rel_err(full[0].cpu().numpy(), h @ W.T) <= TOL
 
 
-def test_single_unit_target_uses_residual_branches(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_single_unit_target_uses_residual_branches(gpu, hd):
     from littlebit_amd.decode import GPUTargetModel
-    cfg = _cfg()
-    st = _state(16, residual=True)
+    cfg = _cfg(hd)
+    st = _state(16, residual=True, hd=hd)
     t = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
     ids = [1, 2, 3, 4]
     lg = t.forward(torch.tensor([ids]))
@@ -316,12 +328,13 @@ def test_single_unit_target_uses_residual_branches(gpu):
     assert O.rel_err(lg[0].cpu().numpy(), ref) <= TOL
 
 
-def test_forward_tree_chain_equals_sequence(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_forward_tree_chain_equals_sequence(gpu, hd):
     """A tree that is one chain verifies like the plain sequence."""
     from littlebit_amd.decode import GPUTargetModel
     from littlebit_amd.tree import generate_tree_buffers
-    cfg = _cfg()
-    st = _state(17)
+    cfg = _cfg(hd)
+    st = _state(17, hd=hd)
     t1 = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
     t2 = GPUTargetModel(draft_state=st, config=cfg, device=gpu, max_seq_len=64)
     prefix = [9, 8, 7, 6]
@@ -333,11 +346,12 @@ def test_forward_tree_chain_equals_sequence(gpu):
     assert t1.draft_unit.cache_pos == len(prefix)
 
 
-def test_speculative_greedy_equals_autoregressive(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_speculative_greedy_equals_autoregressive(gpu, hd):
     from littlebit_amd.decode import GPUDraftModel, GPUTargetModel
     from littlebit_amd.speculative import autoregressive_decode, speculative_decode
-    cfg = _cfg()
-    d, r = _state(18, residual=False), _state(19, residual=False)
+    cfg = _cfg(hd)
+    d, r = _state(18, residual=False, hd=hd), _state(19, residual=False, hd=hd)
     draft = GPUDraftModel(state=d, config=cfg, device=gpu, max_seq_len=96)
     target = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=96)
     ref_t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=96)
@@ -349,12 +363,13 @@ def test_speculative_greedy_equals_autoregressive(gpu):
     assert stats["total_tokens_generated"] == 24
 
 
-def test_speculative_tree_equals_autoregressive(gpu):
+@pytest.mark.parametrize("hd", [32, 64])
+def test_speculative_tree_equals_autoregressive(gpu, hd):
     from littlebit_amd.decode import GPUDraftModel, GPUTargetModel
     from littlebit_amd.speculative import autoregressive_decode, speculative_decode_tree
     from littlebit_amd.tree import generate_tree_buffers, ranked_tree_choices
-    cfg = _cfg()
-    d, r = _state(20, residual=False), _state(21, residual=False)
+    cfg = _cfg(hd)
+    d, r = _state(20, residual=False, hd=hd), _state(21, residual=False, hd=hd)
     draft = GPUDraftModel(state=d, config=cfg, device=gpu, max_seq_len=128, use_graph=False)
     target = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=128)
     ref_t = GPUTargetModel(draft_state=d, residual_state=r, config=cfg, device=gpu, max_seq_len=128)

@@ -448,3 +448,74 @@ def test_fused_silu_mul(gpu, M, x_dtype):
 def test_residual_in_place(gpu, M):
     _fused_run(gpu, M, 512, [(512, [45, 301]), (96, [9])], "rms", residual=True)
     _fused_run(gpu, M, 1000, [(4096, [298])], "silu", residual=True)
+
+
+# --------------------------------------------------------------------------- attention partials as input
+@pytest.mark.parametrize("heads,kvh,hd,max_seq,pos,ranks,device_pos", [
+    (32, 32, 128, 600, 513, [205], True), (32, 32, 128, 600, 513, [205, 1843], False),
+    (16, 4, 64, 100, 15, [64], True), (16, 4, 64, 100, 16, [31, 97], True),
+    (16, 16, 128, 2048, 1500, [300], True), (4, 2, 64, 40, 39, [16], False)])
+def test_attention_merge_input(gpu, heads, kvh, hd, max_seq, pos, ranks, device_pos):
+    """lbk_attention_decode without an output, then a projection reading its
+    partials (LBK_INPUT_ATTN_MERGE) with a residual: the oracle's projection
+    of the float64 attention output, plus the residual; a position past the
+    cache leaves y = residual (the attention reads as zeros)."""
+    import littlebit_amd._lib as L
+    from littlebit_amd import LittleBitProjection
+    from littlebit_amd.ops import AttentionPartials
+    K, N = heads * hd, 384
+    x_unused, brs = _synthetic(4100 + pos, 1, K, N, ranks)
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    g = torch.Generator(device="cpu").manual_seed(pos * 7 + heads)
+    kc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    vc = torch.randn((kvh, max_seq, hd), generator=g).to(gpu)
+    q = torch.randn((heads * hd,), generator=g).to(gpu)
+    k = torch.randn((kvh * hd,), generator=g).to(gpu)
+    v = torch.randn((kvh * hd,), generator=g).to(gpu)
+    res = (torch.randn((1, N), generator=g) * 3).to(gpu)
+    scale = hd ** -0.5
+    K_ = kc.clone().double().cpu()
+    V_ = vc.clone().double().cpu()
+    K_[:, pos] = k.view(kvh, hd).double().cpu()
+    V_[:, pos] = v.view(kvh, hd).double().cpu()
+    rep = heads // kvh
+    s = torch.einsum("grd,gtd->grt", q.view(kvh, rep, hd).double().cpu(), K_[:, :pos + 1]) * scale
+    a_ref = torch.einsum("grt,gtd->grd", torch.softmax(s, dim=-1), V_[:, :pos + 1]).reshape(1, K).numpy()
+    ref = O.littlebit_forward(a_ref, brs, K, N) + res.double().cpu().numpy()
+    lib = L.load()
+    part = torch.empty(lib.lbk_attention_partial_bytes(heads, max_seq, hd) // 4 + 4, device=gpu)
+    for at in ([pos, max_seq] if device_pos else [pos]):
+        pos_t = torch.tensor([at], dtype=torch.int64, device=gpu)
+        print(f"[attn_merge] heads={heads} hd={hd} max_seq={max_seq} pos={at} ranks={ranks} dev={device_pos}",
+              flush=True)
+        rc = lib.lbk_attention_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads,
+                                      kvh, hd, max_seq, pos_t.data_ptr() if device_pos else None,
+                                      0 if device_pos else at, scale, part.data_ptr(), part.numel() * 4, None, None)
+        L.check(rc, "lbk_attention_decode")
+        y = res.clone()
+        proj.forward(None, out=y, residual=y, attn=AttentionPartials(part, hd, max_seq, pos_t if device_pos else None,
+                                                                     0 if device_pos else at))
+        torch.cuda.synchronize()
+        if at < max_seq:
+            err = O.rel_err(y.cpu().numpy(), ref)
+            print(f"[attn_merge] rel_err={err:.2e}", flush=True)
+            assert err <= TOL_F32
+            assert torch.equal(kc[:, at], k.view(kvh, hd))
+        else:
+            assert torch.equal(y, res)
+
+
+def test_attention_merge_input_errors(gpu):
+    import littlebit_amd._lib as L
+    from littlebit_amd import LittleBitProjection
+    from littlebit_amd.ops import AttentionPartials
+    _, brs = _synthetic(11, 1, 512, 64, [16])
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    part = torch.zeros(1 << 16, device=gpu)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        proj.forward(None, attn=AttentionPartials(part, 96, 64, None, 3))
+    odd = LittleBitProjection([_dev_branch(b, gpu) for b in _synthetic(12, 1, 448, 64, [16])[1]])
+    with pytest.raises(RuntimeError, match="heads"):  # K = 448 is no multiple of 128
+        odd.forward(None, attn=AttentionPartials(part, 128, 64, None, 3))
+    with pytest.raises(RuntimeError, match="aligned"):
+        proj.forward(None, attn=AttentionPartials(part[1:], 64, 64, None, 3))
