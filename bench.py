@@ -206,6 +206,38 @@ class PrefillLayer:
                 grp.forward(x, outs=outs)
 
 
+def lm_head_bench(dev, stream, steps=100, warmup=10, copies=4):
+    """The draft step's Q4_0 lm_head + argmax (Llama-2-7B: 32000 x 4096) on
+    its own: ``copies`` quantised weights rotated so that each call reads
+    its planes from HBM (4 x 74 MB > the 256 MB Infinity Cache)."""
+    import torch
+    from littlebit_amd.lm_head import Q4LMHead
+    g = torch.Generator(device="cpu").manual_seed(3)
+    V, H = 32000, 4096
+    heads = []
+    for _ in range(copies):
+        w = torch.randn((V, H), generator=g).to(dev)
+        heads.append(Q4LMHead(w))
+        del w
+    x = torch.randn(H, generator=g).to(dev)
+    nw = torch.ones(H, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            heads[i % copies].argmax(x, nw, 1e-6, out=tok)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(steps):
+            heads[i % copies].argmax(x, nw, 1e-6, out=tok)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / steps
+    nbytes = heads[0].nbytes + 4 * H * 2
+    return {"workload": f"Q4_0 lm_head + argmax, vocab {V} x hidden {H}, final RMSNorm fused, {copies} weight "
+                        "copies rotated (cold)", "us_per_call": round(us, 2), "bytes_per_call": nbytes,
+            "gbs": round(nbytes / us / 1000.0, 1), "launches": 2}
+
+
 def prefill_bench(gen, dev, stream, steps=20, warmup=3):
     """ms per layer and TFLOP/s of the config-4 linears (2 layers' weights rotated)."""
     layers = [PrefillLayer(gen, dev, PREFILL_M) for _ in range(2)]
@@ -255,33 +287,44 @@ def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, tar
     gen = torch.Generator().manual_seed(5)
     # --- config 2: draft model, KV length 512 -------------------------------------
     st = synthetic_runtime_state(cfg, C["draft_rank"], None, seed=1, device=dev)
-    draft = GPUDraftModel(state=st, config=cfg, device=dev, max_seq_len=kv_draft + replays + draft_len + 8,
-                          torch_dtype=torch.bfloat16)
     prompt = torch.randint(0, cfg.vocab_size, (1, kv_draft), generator=gen)
-    draft.generate_draft_tokens(prompt, draft_length=2)  # prefill + builds the graph
-    torch.cuda.synchronize()
-    draft._pos.fill_(kv_draft)
-    for _ in range(3):
-        draft._graph.replay()
-    draft._pos.fill_(kv_draft)
-    a, b = ev()
-    a.record()
-    for _ in range(replays):
-        draft._graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    ms_tok = a.elapsed_time(b) / replays
-    a, b = ev()
-    a.record()
-    draft.generate_draft_tokens(prompt, draft_length=draft_len)
-    b.record()
-    torch.cuda.synchronize()
+
+    def measure_draft(head):
+        draft = GPUDraftModel(state=st, config=cfg, device=dev, max_seq_len=kv_draft + replays + draft_len + 8,
+                              torch_dtype=torch.bfloat16, lm_head=head)
+        draft.generate_draft_tokens(prompt, draft_length=2)  # prefill + builds the graph
+        torch.cuda.synchronize()
+        draft._pos.fill_(kv_draft)
+        for _ in range(3):
+            draft._graph.replay()
+        draft._pos.fill_(kv_draft)
+        a, b = ev()
+        a.record()
+        for _ in range(replays):
+            draft._graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / replays
+        a, b = ev()
+        a.record()
+        draft.generate_draft_tokens(prompt, draft_length=draft_len)
+        b.record()
+        torch.cuda.synchronize()
+        gen_ms = a.elapsed_time(b)
+        del draft
+        torch.cuda.empty_cache()
+        return ms, gen_ms
+
+    ms_tok, gen_ms = measure_draft("q4")
+    ms_dense, _ = measure_draft("dense")
     out["draft"] = {"workload": f"llama2-7b 0.1-bpw draft, one token at KV length {kv_draft}: embedding, 32 layers "
-                                "(norms, attention, 7 LittleBitLinear forwards), final norm, bf16 lm_head, argmax; "
-                                "one HIP graph per token",
+                                "(norms, attention, 7 LittleBitLinear forwards), final norm, Q4_0 lm_head (Q8_0 "
+                                "activations) and argmax as the reference's generate_token; one HIP graph per token",
                     "ms_per_token": round(ms_tok, 4), "tok_per_s": round(1000.0 / ms_tok, 1),
-                    f"generate_draft_tokens_k{draft_len}_ms": round(a.elapsed_time(b), 3)}
-    del draft, st
+                    f"generate_draft_tokens_k{draft_len}_ms": round(gen_ms, 3),
+                    "dense_bf16_lm_head": {"ms_per_token": round(ms_dense, 4),
+                                           "tok_per_s": round(1000.0 / ms_dense, 1)}}
+    del st
     torch.cuda.empty_cache()
     if not target:
         return out
@@ -376,7 +419,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
-    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy"], default=None,
+    ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy",
+                                       "lm_head"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -395,6 +439,9 @@ def main():
     kinds = dict(LAYER_CALLS)
     if args.only == "prefill":
         print(json.dumps(prefill_bench(gen, dev, stream, args.steps, args.warmup)))
+        return
+    if args.only == "lm_head":
+        print(json.dumps(lm_head_bench(dev, stream, args.steps, args.warmup)))
         return
     if args.only == "copy":
         # calibration for the HBM byte counters: a plain device copy of known size

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 5
+#define LBK_ABI_VERSION 6
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -217,6 +217,33 @@ int lbk_unpack_signs(const int32_t* packed, int64_t rows, int64_t cols,
  * (quantization/utils/binary_packer.py:5-51) for inputs in {-1, +1}. */
 int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols,
                    int32_t* out, void* stream);
+
+/* Q4_0 quantisation of an lm_head weight w [rows][cols] fp32 (cols % 32 == 0),
+ * as the reference's quantize_lm_head_q4 (patches/littlebit_cpu_optimized.cpp:
+ * 2129-2149, 2225-2251) computes it, bit for bit: per block of 32 the fp16
+ * scale d = m / -8 (m the first value of largest magnitude; fp16 by
+ * truncation, :2119-2127) and nibbles q = min(15, int(x / d + 8.5)).  Stored
+ * as two planes instead of the reference's 18-byte blocks: qs [rows][cols/2]
+ * (byte j of a block holds value j in its low nibble and value j + 16 in its
+ * high nibble, as the reference packs them; 16-byte aligned) and d
+ * [rows][cols/32] (fp16 bits). */
+int lbk_q4_0_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* qs,
+                      uint16_t* d, void* stream);
+
+/* The tail of the reference's generate_token (patch:2254-2317): the final
+ * hidden state x [hidden] -- RMS-normed first with norm_weight and eps when
+ * norm_weight is not NULL (rms_norm_inline, patch:1370-1405) -- quantised to
+ * Q8_0 (d = amax / 127, q = round(x / d); :2152-2165), the Q4_0 x Q8_0
+ * logits of the vocab rows (:2168-2222; also written to logits [vocab] when
+ * that is not NULL), and the first index of the largest logit written to
+ * *token (device int64).  hidden % 32 == 0, hidden <= 16384; qs, x and
+ * norm_weight 16-byte aligned.  workspace: lbk_lm_head_q4_workspace_bytes(). */
+size_t lbk_lm_head_q4_workspace_bytes(int64_t vocab, int64_t hidden);
+int lbk_lm_head_q4_argmax(const uint8_t* qs, const uint16_t* d, int64_t vocab,
+                          int64_t hidden, const float* x,
+                          const float* norm_weight, float eps, float* logits,
+                          int64_t* token, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -109,6 +109,10 @@ SIGNATURES = {
         [_VP, _I64, _VP, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, ctypes.c_size_t, _VP],
     ),
     "lbk_attention_partial_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "lbk_q4_0_quantize": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP, _VP]),
+    "lbk_lm_head_q4_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "lbk_lm_head_q4_argmax": (ctypes.c_int, [_VP, _VP, _I64, _I64, _VP, _VP, ctypes.c_float, _VP, _VP, _VP,
+                                             ctypes.c_size_t, _VP]),
     "lbk_attention_decode": (
         ctypes.c_int,
         [_VP, _VP, _VP, _VP, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP, _I64,

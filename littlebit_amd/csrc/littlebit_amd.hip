@@ -2037,6 +2037,289 @@ __global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams 
 }
 
 // ---------------------------------------------------------------------------
+// Q4_0 lm_head and argmax: the tail of the reference's generate_token
+// (patches/littlebit_cpu_optimized.cpp:2254-2317).  The weight is quantised
+// once to Q4_0 blocks of 32 (an fp16 scale d = m / -8 for m the block's first
+// value of largest magnitude, nibbles q = min(15, int(x / d + 8.5)), value =
+// (q - 8) * d; :2129-2149), stored here as two planes -- nibbles [V][H/2]
+// (byte j of a block: value j low, value j + 16 high, as the reference packs
+// them) and scales [V][H/32] -- so that every lane load is 16-byte aligned.
+// Per call the final hidden state is (optionally RMS-normed and) quantised
+// to Q8_0 (d = amax / 127, q = round(x / d); :2152-2165), each logit is
+// sum_b fp16(d4_b) * fp16(d8_b) * sum_j (q4_j - 8) * q8_j (:2168-2222) and the
+// token is the first index of the largest logit (:2305-2314).
+// ---------------------------------------------------------------------------
+constexpr int kQK = 32;  // values per Q4_0 / Q8_0 block
+// rows per wave of lm_head_q4_kernel<NBL>: as many as the registers allow,
+// so that the grid fits the chip in one round and fewer blocks repeat the
+// Q8_0 staging
+__host__ __device__ constexpr int head_rows_per_wave(int nbl) { return nbl <= 2 ? 16 : nbl == 4 ? 8 : 4; }
+
+// fp32 -> fp16 bits as the reference converts (patch:2119-2127): exponent
+// rebias, mantissa truncated, below range -> signed zero, above -> infinity
+__device__ __forceinline__ uint32_t fp16_bits_trunc(float f) {
+  const uint32_t v = __float_as_uint(f);
+  const uint32_t sign = (v >> 16) & 0x8000u;
+  const int e = int((v >> 23) & 0xFFu) - 127 + 15;
+  if (e <= 0) return sign;
+  if (e >= 31) return sign | 0x7C00u;
+  return sign | (uint32_t(e) << 10) | ((v >> 13) & 0x3FFu);
+}
+__device__ __forceinline__ float fp16_value(uint32_t h) {  // exact (v_cvt_f32_f16)
+  const uint16_t b = uint16_t(h);
+  _Float16 v;
+  __builtin_memcpy(&v, &b, sizeof(v));
+  return float(v);
+}
+
+// nibble of x for scale reciprocal id: the product and the + 8.5 each
+// rounded to fp32 (no fused multiply-add), then truncated
+__device__ __forceinline__ uint32_t q4_nibble(float x, float id) {
+#pragma clang fp contract(off)
+  const float t = x * id + 8.5f;
+  return uint32_t(min(15, int(t)));
+}
+
+// one thread per block of 32 weights
+__global__ __launch_bounds__(256) void q4_quantize_kernel(const float* __restrict__ w, int64_t nblocks,
+                                                          uint8_t* __restrict__ qs, uint16_t* __restrict__ d) {
+  const int64_t b = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (b >= nblocks) return;
+  const float* x = w + b * kQK;
+  float v[kQK];
+#pragma unroll
+  for (int j = 0; j < kQK / 4; ++j) {
+    const float4 f = *reinterpret_cast<const float4*>(x + 4 * j);
+    v[4 * j] = f.x;
+    v[4 * j + 1] = f.y;
+    v[4 * j + 2] = f.z;
+    v[4 * j + 3] = f.w;
+  }
+  float amax = 0.f, m = 0.f;
+#pragma unroll
+  for (int j = 0; j < kQK; ++j)
+    if (fabsf(v[j]) > amax) {  // strictly greater: the first of equal magnitudes
+      amax = fabsf(v[j]);
+      m = v[j];
+    }
+  const float dv = m / -8.0f;
+  const float id = dv != 0.f ? 1.0f / dv : 0.f;
+  uint32_t words[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t wd = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 4 * k + e;
+      wd |= (q4_nibble(v[j], id) | (q4_nibble(v[j + 16], id) << 4)) << (8 * e);
+    }
+    words[k] = wd;
+  }
+  *reinterpret_cast<uint4*>(qs + b * 16) = uint4{words[0], words[1], words[2], words[3]};
+  d[b] = uint16_t(fp16_bits_trunc(dv));
+}
+
+struct Q4HeadParams {
+  const uint8_t* qs;   // [V][H/2]
+  const uint16_t* d;   // [V][H/32] fp16 bits
+  const float* x;      // [H] final hidden (before the norm when nw is set)
+  const float* nw;     // [H] final RMSNorm weight, or null
+  float eps;
+  int V, H;
+  float* logits;       // [V] or null
+  uint64_t* part;      // [gridDim.x] (value, index) keys of each block's best
+  int64_t* token;      // argmax
+  int nparts;
+};
+
+// larger key = larger logit, then smaller index (the first maximum wins)
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (uint64_t(o) << 32) | uint64_t(0xFFFFFFFFu - uint32_t(idx));
+}
+
+// grid = blocks of 4 waves, head_rows_per_wave(NBL) rows per wave.  Every block first
+// builds the Q8_0 copy of the hidden state in LDS, a thread per block of 32
+// (x, and the norm weight, 16-byte aligned; RMSNorm applied as
+// rms_norm_inline does: x * (1 / sqrt(sum x^2 / H + eps)) * w; patch:1370-1405),
+// while lane l's loads of blocks l, l + 64, .. of each of the wave's rows
+// (one 16-byte nibble load and one scale per block, issued first) are in
+// flight; the dot
+// products on v_dot4_i32_i8 (nibbles 0..15 as signed bytes, minus 8 * sum q8).
+template <int NBL>
+__global__ __launch_bounds__(256) void lm_head_q4_kernel(Q4HeadParams p) {
+  constexpr int HMAX = NBL * 64 * kQK;
+  constexpr int kHeadRowsPerWave = head_rows_per_wave(NBL);
+  __shared__ uint32_t q8w[HMAX / 4];
+  __shared__ float d8[HMAX / kQK];
+  __shared__ int s8[HMAX / kQK];
+  __shared__ float red[4];
+  __shared__ uint64_t best[4];
+  const int tid = int(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+  const int H = p.H, nb = H / kQK;
+  // the wave's rows first: their latency overlaps the staging below
+  const int r0 = (int(blockIdx.x) * 4 + wave) * kHeadRowsPerWave;
+  uint4 wq[kHeadRowsPerWave][NBL];
+  uint32_t wd[kHeadRowsPerWave][NBL];
+#pragma unroll
+  for (int rr = 0; rr < kHeadRowsPerWave; ++rr) {
+    const int r = min(r0 + rr, p.V - 1);
+#pragma unroll
+    for (int i = 0; i < NBL; ++i) {
+      const int b = min(lane + 64 * i, nb - 1);
+      wq[rr][i] = *reinterpret_cast<const uint4*>(p.qs + size_t(r) * (H / 2) + size_t(b) * 16);
+      wd[rr][i] = p.d[size_t(r) * nb + b];
+    }
+  }
+  // Q8_0 of the hidden state: thread t quantises blocks t, t + 256, .. from
+  // its own registers (no cross-lane steps); the RMSNorm's sum of squares is
+  // the one block-wide reduction
+  constexpr int BPT = (HMAX / kQK + 255) / 256;  // Q8 blocks per thread
+  float xv[BPT][kQK], wv[BPT][kQK];
+#pragma unroll
+  for (int c = 0; c < BPT; ++c) {
+    const int b = min(tid + 256 * c, nb - 1);
+#pragma unroll
+    for (int q = 0; q < kQK / 4; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(p.x + b * kQK + 4 * q);
+      xv[c][4 * q] = f.x;
+      xv[c][4 * q + 1] = f.y;
+      xv[c][4 * q + 2] = f.z;
+      xv[c][4 * q + 3] = f.w;
+      if (p.nw) {
+        const float4 g = *reinterpret_cast<const float4*>(p.nw + b * kQK + 4 * q);
+        wv[c][4 * q] = g.x;
+        wv[c][4 * q + 1] = g.y;
+        wv[c][4 * q + 2] = g.z;
+        wv[c][4 * q + 3] = g.w;
+      }
+    }
+  }
+  float rs = 1.f;
+  if (p.nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < BPT; ++c)
+      if (tid + 256 * c < nb) {
+#pragma unroll
+        for (int j = 0; j < kQK; ++j) ss += xv[c][j] * xv[c][j];
+      }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    rs = 1.0f / sqrtf(ss / float(H) + p.eps);
+  }
+#pragma unroll
+  for (int c = 0; c < BPT; ++c) {
+    const int b = tid + 256 * c;
+    if (b >= nb) break;
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) {
+      if (p.nw) xv[c][j] = xv[c][j] * rs * wv[c][j];
+      amax = fmaxf(amax, fabsf(xv[c][j]));
+    }
+    const float dv = amax / 127.0f;
+    const float id = dv != 0.f ? 1.0f / dv : 0.f;
+    uint32_t qw[kQK / 4];
+    int sq = 0;
+#pragma unroll
+    for (int q = 0; q < kQK / 4; ++q) {
+      uint32_t wd4 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = int(roundf(xv[c][4 * q + e] * id));
+        sq += v;
+        wd4 |= (uint32_t(v) & 0xFFu) << (8 * e);
+      }
+      qw[q] = wd4;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(q8w + b * 8);
+    dst[0] = uint4{qw[0], qw[1], qw[2], qw[3]};
+    dst[1] = uint4{qw[4], qw[5], qw[6], qw[7]};
+    d8[b] = fp16_value(fp16_bits_trunc(dv));
+    s8[b] = sq;
+  }
+  __syncthreads();
+  // this lane's blocks of the activation, for every row
+  uint32_t qa[NBL][8];
+  float da[NBL];
+  int sa[NBL];
+#pragma unroll
+  for (int i = 0; i < NBL; ++i) {
+    const int b = min(lane + 64 * i, nb - 1);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) qa[i][k] = q8w[b * 8 + k];
+    da[i] = lane + 64 * i < nb ? d8[b] : 0.f;  // lanes past the row add nothing
+    sa[i] = s8[b];
+  }
+  uint64_t mine = 0;
+#pragma unroll
+  for (int rr = 0; rr < kHeadRowsPerWave; ++rr) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NBL; ++i) {
+      const uint32_t w4[4] = {wq[rr][i].x, wq[rr][i].y, wq[rr][i].z, wq[rr][i].w};
+      int sumi = -8 * sa[i];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        sumi = __builtin_amdgcn_sdot4(int(w4[k] & 0x0F0F0F0Fu), int(qa[i][k]), sumi, false);
+        sumi = __builtin_amdgcn_sdot4(int((w4[k] >> 4) & 0x0F0F0F0Fu), int(qa[i][4 + k]), sumi, false);
+      }
+      acc += (fp16_value(wd[rr][i]) * da[i]) * float(sumi);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    const int r = r0 + rr;
+    if (r < p.V) {
+      if (p.logits && lane == 0) p.logits[r] = acc;
+      const uint64_t k = argmax_key(acc, r);
+      mine = k > mine ? k : mine;
+    }
+  }
+  if (lane == 0) best[wave] = mine;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t m = best[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = best[w] > m ? best[w] : m;
+    p.part[blockIdx.x] = m;
+  }
+}
+
+// one block: the largest key of the blocks' bests -> token
+__global__ __launch_bounds__(256) void argmax_finalize_kernel(Q4HeadParams p) {
+  __shared__ uint64_t red[4];
+  const int tid = int(threadIdx.x);
+  uint64_t m = 0;
+  for (int base = 0; base < p.nparts; base += 256 * 8) {  // eight loads in flight per round
+    uint64_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = base + tid + 256 * k;
+      v[k] = i < p.nparts ? p.part[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = v[k] > m ? v[k] : m;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint64_t other = __shfl_xor(m, o);
+    m = other > m ? other : m;
+  }
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) m = red[w] > m ? red[w] : m;
+    m = red[0] > m ? red[0] : m;
+    *p.token = int64_t(0xFFFFFFFFu - uint32_t(m & 0xFFFFFFFFu));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -2786,6 +3069,79 @@ int lbk_attention_batch(const float* q, const float* k, const float* v, float* k
   if (head_dim == 128) hipLaunchKernelGGL(attn_batch_combine_kernel<128>, cgrid, dim3(128), 0, s, p);
   else hipLaunchKernelGGL(attn_batch_combine_kernel<64>, cgrid, dim3(64), 0, s, p);
   return check_launch("attn_batch_combine_kernel");
+}
+
+int lbk_q4_0_quantize(const float* w, int64_t rows, int64_t cols, uint8_t* qs, uint16_t* d, void* stream) {
+  g_last_error[0] = '\0';
+  if (rows < 0 || cols < 0 || cols % kQK != 0)
+    return set_error(LBK_ERR_ARG, "rows and cols must be >= 0 with cols %% 32 == 0, got %lld x %lld",
+                     (long long)rows, (long long)cols);
+  const int64_t nblocks = rows * (cols / kQK);
+  if (nblocks == 0) return LBK_OK;
+  if (!w || !qs || !d) return set_error(LBK_ERR_ARG, "NULL pointer");
+  if (!aligned16(w) || !aligned16(qs) || (reinterpret_cast<uintptr_t>(d) & 1))
+    return set_error(LBK_ERR_ARG, "w and qs must be 16-byte aligned, d 2-byte aligned");
+  const int64_t grid = ceil_div(nblocks, 256);
+  if (grid > INT_MAX) return set_error(LBK_ERR_ARG, "weight too large");
+  hipLaunchKernelGGL(q4_quantize_kernel, dim3(unsigned(grid)), dim3(256), 0, static_cast<hipStream_t>(stream), w,
+                     nblocks, qs, d);
+  return check_launch("q4_quantize_kernel");
+}
+
+static int head_nbl(int64_t hidden) {
+  const int64_t n = ceil_div(hidden / kQK, 64);
+  return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8;
+}
+
+static int64_t head_blocks(int64_t vocab, int64_t hidden) {
+  return ceil_div(vocab, 4 * head_rows_per_wave(head_nbl(hidden)));
+}
+
+size_t lbk_lm_head_q4_workspace_bytes(int64_t vocab, int64_t hidden) {
+  if (vocab < 1 || hidden < kQK) return 0;
+  return align256(size_t(head_blocks(vocab, hidden)) * sizeof(uint64_t));
+}
+
+int lbk_lm_head_q4_argmax(const uint8_t* qs, const uint16_t* d, int64_t vocab, int64_t hidden, const float* x,
+                          const float* norm_weight, float eps, float* logits, int64_t* token, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  if (vocab < 1 || vocab > INT_MAX - 256)
+    return set_error(LBK_ERR_ARG, "vocab out of range: %lld", (long long)vocab);
+  if (hidden < kQK || hidden % kQK != 0 || hidden > 8 * 64 * kQK)
+    return set_error(LBK_ERR_ARG, "hidden must be a multiple of 32 in [32, %d], got %lld", 8 * 64 * kQK,
+                     (long long)hidden);
+  if (!qs || !d || !x || !token) return set_error(LBK_ERR_ARG, "NULL pointer");
+  if (!aligned16(qs) || !aligned16(x) || (norm_weight && !aligned16(norm_weight)) ||
+      (reinterpret_cast<uintptr_t>(d) & 1))
+    return set_error(LBK_ERR_ARG, "qs, x and norm_weight must be 16-byte aligned, d 2-byte aligned");
+  if (norm_weight && !(eps >= 0.f)) return set_error(LBK_ERR_ARG, "eps must be >= 0");
+  const size_t need = lbk_lm_head_q4_workspace_bytes(vocab, hidden);
+  if (!workspace || workspace_bytes < need)
+    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  Q4HeadParams p;
+  p.qs = qs;
+  p.d = d;
+  p.x = x;
+  p.nw = norm_weight;
+  p.eps = eps;
+  p.V = int(vocab);
+  p.H = int(hidden);
+  p.logits = logits;
+  p.part = static_cast<uint64_t*>(workspace);
+  p.token = token;
+  p.nparts = int(head_blocks(vocab, hidden));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nbl = head_nbl(hidden);
+  const dim3 grid{unsigned(p.nparts)};
+  if (nbl <= 1) hipLaunchKernelGGL(lm_head_q4_kernel<1>, grid, dim3(256), 0, s, p);
+  else if (nbl <= 2) hipLaunchKernelGGL(lm_head_q4_kernel<2>, grid, dim3(256), 0, s, p);
+  else if (nbl <= 4) hipLaunchKernelGGL(lm_head_q4_kernel<4>, grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(lm_head_q4_kernel<8>, grid, dim3(256), 0, s, p);
+  int rc = check_launch("lm_head_q4_kernel");
+  if (rc != LBK_OK) return rc;
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(256), 0, s, p);
+  return check_launch("argmax_finalize_kernel");
 }
 
 }  // extern "C"

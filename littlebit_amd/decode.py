@@ -262,8 +262,10 @@ class LittleBitDecoder:
 
     def forward_hidden(self, x: torch.Tensor, start: int, length: Optional[int] = None,
                        pos_t: Optional[torch.Tensor] = None,
-                       tree_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x [N, hidden] fp32 at positions start.. -> final-norm hidden [N, hidden]."""
+                       tree_mask: Optional[torch.Tensor] = None, final_norm: bool = True) -> torch.Tensor:
+        """x [N, hidden] fp32 at positions start.. -> final-norm hidden [N, hidden]
+        (``final_norm=False``: the residual stream before the final RMSNorm,
+        for a consumer that applies it, such as :class:`Q4LMHead`)."""
         eps = self.config.rms_norm_eps
         if length is None and pos_t is None:
             length = start + x.shape[0]
@@ -276,7 +278,7 @@ class LittleBitDecoder:
                 h = rms_norm(x, L["ln2"], eps)
                 g, u = L["gate_up"].forward(h)
                 x = x + L["down"].forward(F.silu(g) * u)
-            return rms_norm(x, self.final_norm, eps)
+            return rms_norm(x, self.final_norm, eps) if final_norm else x
         # the norms, SiLU * up and the residual adds run inside the projection
         # calls; x (a private copy) is updated in place by o and down
         x = x.to(torch.float32).clone()
@@ -290,10 +292,10 @@ class LittleBitDecoder:
                 L["o"].forward(a, out=x, residual=x)
             g, u = L["gate_up"].forward(x, rms_weight=L["ln2"], rms_eps=eps)
             L["down"].forward(g, out=x, residual=x, x_up=u)
-        return rms_norm(x, self.final_norm, eps)
+        return rms_norm(x, self.final_norm, eps) if final_norm else x
 
     def forward_batch(self, token_ids: Sequence[int], embed_tokens: torch.Tensor,
-                      tree_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      tree_mask: Optional[torch.Tensor] = None, final_norm: bool = True) -> torch.Tensor:
         """N tokens at positions cache_pos.. (causal, or ``tree_mask``);
         advances cache_pos by N.  Returns final-norm hidden [N, hidden]
         (the reference's _LBModelUnit.forward_batch, cpu_target_model.py:325-368)."""
@@ -304,13 +306,13 @@ class LittleBitDecoder:
             raise RuntimeError(f"KV cache full: {self.cache_pos} + {n} > max_seq_len {self.max_seq_len}")
         ids = torch.as_tensor(list(token_ids), dtype=torch.long, device=self.device)
         x = embed_tokens.index_select(0, ids).to(torch.float32)
-        out = self.forward_hidden(x, self.cache_pos, tree_mask=tree_mask)
+        out = self.forward_hidden(x, self.cache_pos, tree_mask=tree_mask, final_norm=final_norm)
         self.cache_pos += n
         return out
 
-    def forward_token(self, token_id: int, embed_tokens: torch.Tensor) -> torch.Tensor:
+    def forward_token(self, token_id: int, embed_tokens: torch.Tensor, final_norm: bool = True) -> torch.Tensor:
         """One token; returns final-norm hidden [1, hidden] (cpu_target_model.py:240-323)."""
-        return self.forward_batch([token_id], embed_tokens)
+        return self.forward_batch([token_id], embed_tokens, final_norm=final_norm)
 
 
 def _embed_and_head(state: Dict[str, torch.Tensor], dev, embed_tokens, lm_head_weight, base_model_id, dtype):
@@ -362,22 +364,41 @@ class GPUDraftModel:
     HIP graph that feeds its argmax back as the next input, so greedy drafts
     run without host round trips; attention then spans the whole cache with
     later positions masked, so size ``max_seq_len`` to the context.
+
+    ``lm_head="q4"`` (the default) is the reference's C++ draft path
+    (generate_token, cpu_draft_model.py:485-563): the lm_head quantised to
+    Q4_0, the hidden state to Q8_0, the token their argmax, the returned
+    probabilities one-hot at it, whatever ``greedy`` and ``temperature`` say.
+    ``lm_head="dense"`` is its Python fallback (:565-584): ``F.linear`` in
+    ``torch_dtype``, softmax probabilities, greedy or sampled tokens.
     """
 
     def __init__(self, runtime_path: Optional[str] = None, base_model_id: Optional[str] = None,
                  torch_dtype=torch.float32, *, state: Optional[Dict[str, torch.Tensor]] = None,
                  config=None, embed_tokens: Optional[torch.Tensor] = None,
                  lm_head_weight: Optional[torch.Tensor] = None, device="cuda", max_seq_len: int = 4096,
-                 use_graph: bool = True):
+                 use_graph: bool = True, lm_head: str = "q4"):
+        if lm_head not in ("q4", "dense"):
+            raise ValueError(f"lm_head must be 'q4' or 'dense', got {lm_head!r}")
         state, config = _load_state(runtime_path, state, config)
         dev = torch.device(device)
         self.config = config
         self.device = dev
         self.max_seq_len = int(max_seq_len)
+        self.lm_head_mode = lm_head
         self.unit = LittleBitDecoder(state, config, dev, max_seq_len, residual=False)
-        self.embed_tokens, self.lm_head_weight = _embed_and_head(state, dev, embed_tokens, lm_head_weight,
-                                                                 base_model_id, torch_dtype)
-        self._vocab_size = int(self.lm_head_weight.shape[0])
+        q4 = lm_head == "q4"
+        self.embed_tokens, head = _embed_and_head(state, dev, embed_tokens, lm_head_weight, base_model_id,
+                                                  torch.float32 if q4 else torch_dtype)
+        self._vocab_size = int(head.shape[0])
+        self._q4 = None
+        self.lm_head_weight = None
+        if q4:
+            from .lm_head import Q4LMHead
+            self._q4 = Q4LMHead(head)  # quantised from the fp32 weight, which is then dropped
+            del head
+        else:
+            self.lm_head_weight = head
         self._cache_pos = 0
         self._cached_seq_len = 0
         self._last_hidden = None
@@ -395,11 +416,26 @@ class GPUDraftModel:
     def _lm_head(self, hidden: torch.Tensor) -> torch.Tensor:
         return F.linear(hidden.to(self.lm_head_weight.dtype), self.lm_head_weight).to(torch.float32)
 
+    def _head_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """Logits [1, vocab] fp32 of a final hidden state as this model holds
+        it (before the final norm with the Q4_0 head, after it with dense)."""
+        if self._q4 is None:
+            return self._lm_head(hidden)
+        logits = torch.empty((1, self._vocab_size), dtype=torch.float32, device=self.device)
+        self._q4.argmax(hidden, self.unit.final_norm, self.config.rms_norm_eps, logits=logits)
+        return logits
+
+    def _q4_token(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Token of a pre-norm hidden state: final RMSNorm, Q8_0, Q4_0 logits,
+        argmax (generate_token's tail, patch:2276-2314), on the device."""
+        return self._q4.argmax(hidden, self.unit.final_norm, self.config.rms_norm_eps, out=out)
+
     @torch.no_grad()
     def _forward_token(self, token_id: int) -> torch.Tensor:
-        """One token at _cache_pos (committed); returns final hidden [1, hidden]."""
+        """One token at _cache_pos (committed); returns final hidden [1, hidden]
+        (before the final norm with the Q4_0 head, which applies it)."""
         self.unit.cache_pos = self._cache_pos
-        h = self.unit.forward_token(token_id, self.embed_tokens)
+        h = self.unit.forward_token(token_id, self.embed_tokens, final_norm=self._q4 is None)
         self._cache_pos += 1
         self._last_hidden = h
         return h
@@ -408,18 +444,23 @@ class GPUDraftModel:
         dev = self.device
         self._tok = torch.zeros(1, dtype=torch.long, device=dev)
         self._pos = torch.zeros(1, dtype=torch.long, device=dev)
-        self._out_tok = torch.zeros(1, dtype=torch.long, device=dev)
-        self._out_logits = torch.zeros((1, self._vocab_size), dtype=torch.float32, device=dev)
+        if self._q4 is None:
+            self._out_tok = torch.zeros(1, dtype=torch.long, device=dev)
+            self._out_logits = torch.zeros((1, self._vocab_size), dtype=torch.float32, device=dev)
         stream = torch.cuda.Stream(device=dev)
 
         def step():
             x = self.embed_tokens.index_select(0, self._tok)
-            h = self.unit.forward_hidden(x, 0, pos_t=self._pos)
-            logits = self._lm_head(h)
-            self._out_logits.copy_(logits)
-            nxt = torch.argmax(logits, dim=-1)
-            self._out_tok.copy_(nxt)
-            self._tok.copy_(nxt)
+            if self._q4 is not None:  # norm, Q4_0 head and argmax in two launches; the token is the next input
+                h = self.unit.forward_hidden(x, 0, pos_t=self._pos, final_norm=False)
+                self._q4_token(h, out=self._tok)
+            else:
+                h = self.unit.forward_hidden(x, 0, pos_t=self._pos)
+                logits = self._lm_head(h)
+                self._out_logits.copy_(logits)
+                nxt = torch.argmax(logits, dim=-1)
+                self._out_tok.copy_(nxt)
+                self._tok.copy_(nxt)
             self._pos.add_(1)
 
         # The warm run really executes: it writes KV at _pos, so it runs at
@@ -453,8 +494,8 @@ class GPUDraftModel:
         ids = input_ids[0, start:seq_len].tolist()
         if ids:
             self.unit.cache_pos = start
-            h = self.unit.forward_batch(ids, self.embed_tokens)
-            self._prompt_hidden = h[-1:]
+            h = self.unit.forward_batch(ids, self.embed_tokens, final_norm=self._q4 is None)
+            self._prompt_hidden = h[-1:].contiguous()
         self._last_hidden = self._prompt_hidden
         self._cache_pos = seq_len
         self._cached_seq_len = seq_len
@@ -470,7 +511,32 @@ class GPUDraftModel:
         cache_pos_before_draft = self._cache_pos
         tokens: List[torch.Tensor] = []
         probs: List[torch.Tensor] = []
-        if draft_length > 0 and greedy and self.use_graph:
+        if draft_length > 0 and self._q4 is not None:
+            # generate_token per draft position: argmax of the Q4_0 logits,
+            # one-hot probabilities (cpu_draft_model.py:526-563)
+            if self._cache_pos + draft_length > self.max_seq_len:
+                raise RuntimeError("KV cache full")
+            first = self._q4_token(self._last_hidden)
+            outs = [first.clone()]
+            if draft_length > 1 and self.use_graph:
+                if self._graph is None:
+                    self._build_graph()
+                self._tok.copy_(first)
+                self._pos.fill_(self._cache_pos)
+                for _ in range(draft_length - 1):
+                    self._graph.replay()
+                    outs.append(self._tok.clone())
+                toks = torch.cat(outs).cpu().tolist()
+            else:
+                toks = [int(first.item())]
+                for _ in range(draft_length - 1):
+                    toks.append(int(self._q4_token(self._forward_token(toks[-1])).item()))
+            for t in toks:
+                tokens.append(torch.tensor([[t]], dtype=torch.long))
+                p = torch.zeros(1, self._vocab_size)
+                p[0, t] = 1.0
+                probs.append(p.unsqueeze(0))
+        elif draft_length > 0 and greedy and self.use_graph:
             if self._cache_pos + draft_length > self.max_seq_len:
                 raise RuntimeError("KV cache full")
             if self._graph is None:

@@ -141,12 +141,13 @@ def evaluate_posterior_greedy(logits: torch.Tensor, candidates: torch.Tensor):
 def generate_draft_tree(draft, input_ids: torch.Tensor, tree_buffers: Dict, top_k: int = 10) -> torch.Tensor:
     """Tokens of every tree node (1, T) from a GPUDraftModel: the root is the
     last prompt token, the k-th child of a node is the draft's k-th most
-    likely token after the node's path (tree_utils.py:314-494)."""
+    likely token after the node's path (tree_utils.py:314-494), ranked by the
+    draft's own head (the Q4_0 logits when it uses the Q4_0 head)."""
     paths = [tuple(p) for p in tree_buffers["sorted_tree_choices"]]
     need = {p[:d] for p in paths for d in range(1, len(p))}
     draft.prefill(input_ids)
     prefix = int(input_ids.shape[1])
-    root_logits = draft._lm_head(draft._last_hidden)
+    root_logits = draft._head_logits(draft._last_hidden)
     k_max = max(max(p) for p in paths) + 1
     if k_max > top_k:
         raise ValueError(f"tree needs top_k >= {k_max}")
@@ -157,8 +158,8 @@ def generate_draft_tree(draft, input_ids: torch.Tensor, tree_buffers: Dict, top_
         if p in need:
             ids = [tokens[p[:d]] for d in range(1, len(p) + 1)]
             draft.unit.cache_pos = prefix
-            h = draft.unit.forward_batch(ids, draft.embed_tokens)
-            children[p] = torch.topk(draft._lm_head(h[-1:])[0], k_max).indices.tolist()
+            h = draft.unit.forward_batch(ids, draft.embed_tokens, final_norm=draft._q4 is None)
+            children[p] = torch.topk(draft._head_logits(h[-1:].contiguous())[0], k_max).indices.tolist()
     draft.unit.cache_pos = prefix
     out = [int(input_ids[0, -1])] + [tokens[p] for p in paths]
     return torch.tensor([out], dtype=torch.long)

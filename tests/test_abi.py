@@ -209,3 +209,26 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(L.LittleBitLibraryMissing):
         L.load()
+
+
+def test_q4_head_argument_errors():
+    import littlebit_amd._lib as L
+    lib = L.load()
+    assert lib.lbk_q4_0_quantize(0x1000, 2, 33, 0x1000, 0x1000, None) == L.LBK_ERR_ARG  # cols % 32
+    assert lib.lbk_q4_0_quantize(0x1004, 2, 32, 0x1000, 0x1000, None) == L.LBK_ERR_ARG  # alignment
+    assert "aligned" in L.last_error()
+    assert lib.lbk_q4_0_quantize(None, 0, 32, None, None, None) == L.LBK_OK  # nothing to do
+    assert lib.lbk_lm_head_q4_workspace_bytes(0, 4096) == 0
+    need = lib.lbk_lm_head_q4_workspace_bytes(32000, 4096)
+    assert need >= 500 * 8  # one argmax key per block of 64 rows
+    fx = lib.lbk_lm_head_q4_argmax
+    assert fx(0x1000, 0x1000, 100, 48, 0x1000, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert "multiple of 32" in L.last_error()
+    assert fx(0x1000, 0x1000, 100, 32768, 0x1000, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1000, 0x1000, 0, 64, 0x1000, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1008, 0x1000, 100, 64, 0x1000, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1000, 0x1000, 100, 64, 0x1000, 0x1000, -1.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1000, 0x1000, 32000, 4096, 0x1000, None, 0.0, None, 0x1000, 0x1000, 8, None) == L.LBK_ERR_WORKSPACE
+    assert fx(0x1000, 0x1000, 100, 64, None, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1000, 0x1000, 100, 64, 0x1004, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+    assert fx(0x1000, 0x1000, 100, 64, 0x1000, 0x1008, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG

@@ -271,12 +271,13 @@ def test_batch_equals_token_by_token(gpu, hd):
 
 
 @pytest.mark.parametrize("hd", [32, 64])
-def test_draft_graph_equals_eager_and_rolls_back(gpu, hd):
+@pytest.mark.parametrize("head", ["q4", "dense"])
+def test_draft_graph_equals_eager_and_rolls_back(gpu, hd, head):
     from littlebit_amd.decode import GPUDraftModel
     cfg = _cfg(hd)
     st = _state(13, residual=False, hd=hd)
-    g = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=True)
-    e = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False)
+    g = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=True, lm_head=head)
+    e = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False, lm_head=head)
     prompt = torch.tensor([[1, 44, 90, 200, 3]])
     for rnd in range(3):
         tg, pg = g.generate_draft_tokens(prompt, draft_length=6)
@@ -289,7 +290,7 @@ def test_draft_graph_equals_eager_and_rolls_back(gpu, hd):
         # next prompt = accepted drafts + one more token: only the new part is computed
         prompt = torch.cat([prompt, torch.tensor([[int(tg[0]), int(tg[1]), 77]])], dim=1)
     # a fresh model on the final prompt drafts the same tokens
-    f = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False)
+    f = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, use_graph=False, lm_head=head)
     assert [int(t) for t in f.generate_draft_tokens(prompt, draft_length=4)[0]] == \
            [int(t) for t in g.generate_draft_tokens(prompt, draft_length=4)[0]]
 
@@ -379,3 +380,27 @@ def test_speculative_tree_equals_autoregressive(gpu, hd):
                                          eos_token_id=-1)
     ref = autoregressive_decode(ref_t, prompt, 16, eos_token_id=-1)
     assert out.tolist() == ref.tolist()
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+def test_q4_draft_tokens_follow_generate_token(gpu, hd):
+    """The Q4_0 draft path (the reference's generate_token): each draft
+    token is the Q4_0 x Q8_0 argmax of the previous position's final hidden
+    state (oracle on the float64 reference decoder's hidden), and the
+    probabilities are one-hot at it (cpu_draft_model.py:541-563)."""
+    from littlebit_amd.decode import GPUDraftModel
+    from oracle import lm_head_q4_oracle as Q
+    cfg = _cfg(hd)
+    st = _state(23, residual=False, hd=hd)
+    m = GPUDraftModel(state=st, config=cfg, device=gpu, max_seq_len=48, lm_head="q4")
+    prompt = [5, 9, 100, 7]
+    toks, probs = m.generate_draft_tokens(torch.tensor([prompt]), draft_length=4)
+    toks = [int(t) for t in toks]
+    qs, d = Q.quantize_q4_0(st["lm_head.weight"].float().numpy())
+    seq = list(prompt)
+    for t, p in zip(toks, probs):
+        assert p.shape == (1, 1, cfg.vocab_size) and float(p[0, 0, t]) == 1.0 and float(p.sum()) == 1.0
+        h = ref_hidden(st, cfg, seq, False)[-1].astype(np.float32)
+        logits, _ = Q.generate_token_head(h, qs, d)
+        assert logits[t] >= logits.max() - 2e-3 * np.abs(logits).max(), (seq, t)
+        seq.append(t)
