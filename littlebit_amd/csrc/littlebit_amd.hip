@@ -1615,155 +1615,129 @@ struct AttnParams {
 
 __device__ __forceinline__ int64_t attn_pos(const AttnParams& p) { return p.pos_ptr ? *p.pos_ptr : p.pos; }
 
+// One wave per 16-position chunk, no barriers: grid = (heads, ceil(chunks / 4)),
+// wave w of block (h, C) takes chunk 4 C + w.  K rows load LPR lanes per row
+// (4 dims each), RPI rows per instruction; the NI partial dots of a lane are
+// summed over its row's LPR lanes by a halving butterfly (each step sends half
+// of the remaining values, so lane l ends with the full score of one row,
+// held by 4 lanes); the chunk's max and exp-sum are wave reductions; p . V
+// broadcasts each row's weight with v_readlane from a lane fixed at compile
+// time, every lane accumulating its DPL dims over the 16 rows.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p) {
-  // scores: LPR lanes read one K row (4 dims each) and reduce by shuffles, so
-  // a wave's load covers RPI whole rows; each wave takes PW positions.
-  // p . V: each wave takes the same PW positions, a lane DPL dimensions.
-  constexpr int LPR = HD / 4, RPI = 64 / LPR, NW = kAttnThreads / 64, PW = kAttnChunk / NW, DPL = HD / 64;
+  constexpr int LPR = HD / 4, RPI = 64 / LPR, NI = kAttnChunk / RPI, DPL = HD / 64;
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
-  const int h = int(blockIdx.x), c = int(blockIdx.y), tid = int(threadIdx.x);
-  const int wave = tid >> 6, lane = tid & 63;
+  static_assert(NI == 8 || NI == 4, "rows per instruction");
+  const int h = int(blockIdx.x), wave = int(threadIdx.x) >> 6, lane = int(threadIdx.x) & 63;
+  const int c = int(blockIdx.y) * 4 + wave;
   const int kv = h / p.rep;
   const int64_t pos = attn_pos(p);
-  float* part = p.part + (size_t(h) * p.chunks + c) * (HD + kAttnPad);
   if (pos < 0 || pos >= p.max_seq) {  // out of range: nothing is read or stored
-    if (p.out && c == 0 && tid < HD) p.out[size_t(h) * HD + tid] = 0.f;
-    return;
-  }
-  const int S = int(pos) + 1;
-  const int t0 = c * kAttnChunk, t1 = min(t0 + kAttnChunk, S);
-  if (t0 >= t1) {  // chunk past the current length: an empty partial
-    if (tid < HD) part[tid] = 0.f;
-    if (tid == 0) {
-      part[HD] = -INFINITY;
-      part[HD + 1] = 0.f;
+    if (p.out && c == 0) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) p.out[size_t(h) * HD + lane * DPL + j] = 0.f;
     }
     return;
   }
+  const int S = int(pos) + 1;
+  const int t0 = c * kAttnChunk;
+  if (c >= p.chunks || t0 >= S) return;  // chunk past the current length: takes no part
   const float* kn = p.k + size_t(kv) * HD;
   const float* vn = p.v + size_t(kv) * HD;
   float* kc = p.kc + size_t(kv) * p.max_seq * HD;
   float* vc = p.vc + size_t(kv) * p.max_seq * HD;
-  if (c == 0 && (h % p.rep) == 0 && tid < HD) {  // store the new key / value (read below from kn, vn)
-    kc[size_t(pos) * HD + tid] = kn[tid];
-    vc[size_t(pos) * HD + tid] = vn[tid];
-  }
-  __shared__ float ps[kAttnChunk];
-  __shared__ float wred[NW];
-  __shared__ float ored[NW][HD];
-  const bool full = t1 - t0 == kAttnChunk && !(pos >= t0 && pos < t1);  // no tail, no new row
-  const int d0 = lane * DPL;
-  float vv[PW][DPL];  // a full chunk's V rows, loaded before anything waits
-  if (full) {
+  if (c == 0 && (h % p.rep) == 0) {  // store the new key / value (read below from kn, vn)
 #pragma unroll
-    for (int it = 0; it < PW; ++it) {
-      const float* vr = vc + size_t(t0 + wave * PW + it) * HD + d0;
-      if constexpr (DPL == 2) {
-        const float2 w2 = *reinterpret_cast<const float2*>(vr);
-        vv[it][0] = w2.x;
-        vv[it][DPL - 1] = w2.y;
-      } else {
-        vv[it][0] = vr[0];
-      }
+    for (int j = 0; j < DPL; ++j) {
+      kc[size_t(pos) * HD + lane * DPL + j] = kn[lane * DPL + j];
+      vc[size_t(pos) * HD + lane * DPL + j] = vn[lane * DPL + j];
     }
   }
-  // each lane's 4 query dims straight from memory (no LDS, no barrier), so
-  // the K loads below issue right behind it
+  // every load first: K rows, V rows, the query (rows past the length read row t0)
   const int sub = lane / LPR, dl = (lane % LPR) * 4;
-  float4 q4 = *reinterpret_cast<const float4*>(p.q + size_t(h) * HD + dl);
-  q4.x *= p.scale;
-  q4.y *= p.scale;
-  q4.z *= p.scale;
-  q4.w *= p.scale;
-  if (full) {  // every load first, then the arithmetic
-    float4 kk[PW / RPI];
+  float4 kk[NI];
 #pragma unroll
-    for (int it = 0; it < PW / RPI; ++it)
-      kk[it] = *reinterpret_cast<const float4*>(kc + size_t(t0 + wave * PW + it * RPI + sub) * HD + dl);
+  for (int i = 0; i < NI; ++i) {
+    const int t = t0 + i * RPI + sub;
+    const float* kr = t == pos ? kn : kc + size_t(t < S ? t : t0) * HD;
+    kk[i] = *reinterpret_cast<const float4*>(kr + dl);
+  }
+  float vv[kAttnChunk][DPL];
 #pragma unroll
-    for (int it = 0; it < PW / RPI; ++it) {
-      float d = q4.x * kk[it].x + q4.y * kk[it].y + q4.z * kk[it].z + q4.w * kk[it].w;
-#pragma unroll
-      for (int o = LPR / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
-      if ((lane % LPR) == 0) ps[wave * PW + it * RPI + sub] = d;
-    }
-  } else {
-#pragma unroll
-    for (int it = 0; it < PW / RPI; ++it) {
-      const int i = wave * PW + it * RPI + sub;
-      const int t = t0 + i;
-      float d = 0.f;
-      if (t < t1) {
-        const float* kr = (t == pos) ? kn : kc + size_t(t) * HD;
-        const float4 kk = *reinterpret_cast<const float4*>(kr + dl);
-        d = q4.x * kk.x + q4.y * kk.y + q4.z * kk.z + q4.w * kk.w;
-      }
-#pragma unroll
-      for (int o = LPR / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
-      if ((lane % LPR) == 0) ps[i] = (t < t1) ? d : -INFINITY;
+  for (int r = 0; r < kAttnChunk; ++r) {
+    const int t = t0 + r;
+    const float* vr = (t == pos ? vn : vc + size_t(t < S ? t : t0) * HD) + lane * DPL;
+    if constexpr (DPL == 2) {
+      const float2 w2 = *reinterpret_cast<const float2*>(vr);
+      vv[r][0] = w2.x;
+      vv[r][DPL - 1] = w2.y;
+    } else {
+      vv[r][0] = vr[0];
     }
   }
-  __syncthreads();
-  // chunk max and exp-sum (threads 0 .. kAttnChunk-1 hold one position each)
-  const float sc = tid < kAttnChunk ? ps[tid] : -INFINITY;
+  const float4 q4 = *reinterpret_cast<const float4*>(p.q + size_t(h) * HD + dl);
+  float v[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    v[i] = (q4.x * kk[i].x + q4.y * kk[i].y + q4.z * kk[i].z + q4.w * kk[i].w) * p.scale;
+  // halving butterfly over the LPR lanes of a row: masks LPR/2 .. 4 halve NI
+  // values down to one (index bits taken from the lane), masks 2 and 1 sum
+#pragma unroll
+  for (int m = LPR / 2, n = NI; m >= 1; m >>= 1) {
+    if (n > 1) {
+      const bool up = (lane & m) != 0;
+#pragma unroll
+      for (int j = 0; j < NI / 2; ++j) {
+        if (j < n / 2) {
+          const float send = up ? v[j] : v[j + n / 2];
+          const float keep = up ? v[j + n / 2] : v[j];
+          v[j] = keep + __shfl_xor(send, m);
+        }
+      }
+      n /= 2;
+    } else {
+      v[0] += __shfl_xor(v[0], m);
+    }
+  }
+  // this lane's row: index bits from the halving masks, then the instruction's row
+  int irow = 0;
+#pragma unroll
+  for (int m = LPR / 2, n = NI; n > 1; m >>= 1, n >>= 1) irow = 2 * irow + ((lane & m) ? 1 : 0);
+  const int row = irow * RPI + sub;
+  const float sc = t0 + row < S ? v[0] : -INFINITY;
   float mx = sc;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) wred[wave] = mx;
-  __syncthreads();
-  mx = wred[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, wred[w]);
-  const float e = (tid < kAttnChunk && t0 + tid < t1) ? __expf(sc - mx) : 0.f;
-  float sm = e;
+  const float e = t0 + row < S ? __expf(sc - mx) : 0.f;
+  float sm = 0.25f * e;  // every row is held by 4 lanes
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sm += __shfl_xor(sm, o);
-  __syncthreads();  // every thread has read wred (max) and ps (scores)
-  if (tid < kAttnChunk) ps[tid] = e;
-  if (lane == 0) wred[wave] = sm;
-  __syncthreads();
-  sm = 0.f;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) sm += wred[w];
-  // p . V over this wave's positions
   float o[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) o[j] = 0.f;
-  if (full) {
 #pragma unroll
-    for (int it = 0; it < PW; ++it) {
-      const float pi = ps[wave * PW + it];
+  for (int r = 0; r < kAttnChunk; ++r) {
+    // a lane holding row r: instruction row i = r / RPI at sub r % RPI, i's
+    // bits at the halving masks (lowest mask for the lowest bit), bits 2, 1 zero
+    const int ir = r / RPI, sr = r % RPI;
+    int ln = sr * LPR;
+    int mbit = 4;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) o[j] += pi * vv[it][j];
-    }
-  } else {
-    for (int it = 0; it < PW; ++it) {
-      const int i = wave * PW + it;
-      const int t = t0 + i;
-      if (t < t1) {
-        const float* vr = (t == pos) ? vn : vc + size_t(t) * HD;
-        const float pi = ps[i];
+    for (int n = NI, k = 0; n > 1; n >>= 1, ++k, mbit <<= 1) ln |= ((ir >> k) & 1) ? mbit : 0;
+    const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), ln));
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) o[j] += pi * vr[d0 + j];
-      }
-    }
+    for (int j = 0; j < DPL; ++j) o[j] += pr * vv[r][j];
   }
+  float* part = p.part + (size_t(h) * p.chunks + c) * (HD + kAttnPad);
+  if (p.chunks == 1 && p.out) {
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) ored[wave][d0 + j] = o[j];
-  __syncthreads();
-  if (tid < HD) {
-    float od = 0.f;
+    for (int j = 0; j < DPL; ++j) p.out[size_t(h) * HD + lane * DPL + j] = o[j] / sm;
+  } else {
 #pragma unroll
-    for (int w = 0; w < NW; ++w) od += ored[w][tid];
-    if (p.chunks == 1 && p.out) {
-      p.out[size_t(h) * HD + tid] = od / sm;
-    } else {
-      part[tid] = od;
-      if (tid == 0) {
-        part[HD] = mx;
-        part[HD + 1] = sm;
-      }
+    for (int j = 0; j < DPL; ++j) part[lane * DPL + j] = o[j];
+    if (lane == 0) {
+      part[HD] = mx;
+      part[HD + 1] = sm;
     }
   }
 }
@@ -2988,7 +2962,7 @@ int lbk_attention_decode(const float* q, const float* k, const float* v, float* 
   p.part = partial;
   p.out = out;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid{unsigned(heads), unsigned(chunks), 1u};
+  const dim3 grid{unsigned(heads), unsigned(ceil_div(chunks, kAttnThreads / 64)), 1u};
   if (head_dim == 128) hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(kAttnThreads), 0, s, p);
   else hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(kAttnThreads), 0, s, p);
   int rc = check_launch("attn_decode_kernel");
