@@ -144,9 +144,9 @@ struct Raw8<uint16_t> {
 // MFMA path parameters
 // ---------------------------------------------------------------------------
 constexpr int kMaxWaveSteps = 32;  // rank steps (both branches) per expand wave
-// positions per block of the decode attention: more, smaller blocks measured
-// faster at KV 512 than 32 or 64; its partials are rows of kAttnPad + head_dim
-// floats (o, then max and exp-sum, 16-byte aligned rows)
+// positions per wave of the decode attention (16 measured faster at KV 512
+// than 8 or 32); its partials are rows of head_dim + kAttnPad floats (o, then
+// max and exp-sum, 16-byte aligned rows)
 constexpr int kAttnChunk = 16;
 constexpr int kAttnPad = 4;
 constexpr int kMaxProj = 4;        // projections sharing one input in a group call
@@ -1626,8 +1626,9 @@ __device__ __forceinline__ int64_t attn_pos(const AttnParams& p) { return p.pos_
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p) {
   constexpr int LPR = HD / 4, RPI = 64 / LPR, NI = kAttnChunk / RPI, DPL = HD / 64;
+  constexpr int COPIES = LPR / NI;  // lanes left holding each row's score (the summing masks)
   static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
-  static_assert(NI == 8 || NI == 4, "rows per instruction");
+  static_assert(NI >= 2 && NI <= LPR && (NI & (NI - 1)) == 0, "rows per instruction");
   const int h = int(blockIdx.x), wave = int(threadIdx.x) >> 6, lane = int(threadIdx.x) & 63;
   const int c = int(blockIdx.y) * 4 + wave;
   const int kv = h / p.rep;
@@ -1709,7 +1710,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   const float e = t0 + row < S ? __expf(sc - mx) : 0.f;
-  float sm = 0.25f * e;  // every row is held by 4 lanes
+  float sm = e * (1.0f / COPIES);  // every row is held by COPIES lanes
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sm += __shfl_xor(sm, o);
   float o[DPL];
@@ -1718,10 +1719,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
 #pragma unroll
   for (int r = 0; r < kAttnChunk; ++r) {
     // a lane holding row r: instruction row i = r / RPI at sub r % RPI, i's
-    // bits at the halving masks (lowest mask for the lowest bit), bits 2, 1 zero
+    // bits at the halving masks (the lowest, COPIES, for the lowest bit), the
+    // summing-mask bits zero
     const int ir = r / RPI, sr = r % RPI;
     int ln = sr * LPR;
-    int mbit = 4;
+    int mbit = COPIES;
 #pragma unroll
     for (int n = NI, k = 0; n > 1; n >>= 1, ++k, mbit <<= 1) ln |= ((ir >> k) & 1) ? mbit : 0;
     const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), ln));
