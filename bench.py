@@ -392,21 +392,32 @@ def cpu_baseline(layers, budget_s=12.0):
             ops.littlebit_linear(x, b.v2.reshape(1, K), b.v_sign, K, b.mid.reshape(1, R), b.u_sign, R,
                                  b.u1.reshape(1, N))
 
-    one_step()
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
+    def timed(budget):
         one_step()
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 100000:
-            break
+        t0 = time.perf_counter()
+        steps = 0
+        while True:
+            one_step()
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget or steps >= 100000:
+                return steps, el
+
+    steps, el = timed(budget_s)
     ms_step = el / steps * 1000.0
+    # the reference's own run scripts use 4 threads (eval_speculative_matryoshka_cpu.sh:45-57)
+    torch.set_num_threads(4)
+    steps4, el4 = timed(budget_s / 2)
+    torch.set_num_threads(threads)
+    ms4 = el4 / steps4 * 1000.0
     return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
             "ms_per_step": round(ms_step, 3), "tok_per_s_linears": round(1000.0 / ms_step, 2),
+            "threads_4": {"value": round(step_bytes * steps4 / el4 / 1e9, 3), "ms_per_step": round(ms4, 3),
+                          "steps": steps4},
             "sample": (f"littlebit_cpu_ops::littlebit_linear (reference AVX2 kernel, int8 activations) over "
                        f"{steps} whole draft steps ({layers} layers x 7 projections, distinct weights, "
-                       f"{step_bytes / 2**20:.0f} MiB per step) in {el:.1f} s; torch intra-op threads = {threads}")}
+                       f"{step_bytes / 2**20:.0f} MiB per step) in {el:.1f} s; torch intra-op threads = {threads}; "
+                       f"threads_4: the same with 4 threads, {steps4} steps in {el4:.1f} s")}
 
 
 def main():
