@@ -1747,6 +1747,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnParams p)
 // out[h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c, M the
 // largest m_c: one pass for M, one for the sums, so that every chunk's loads
 // are independent (a running maximum would chain them).  grid = heads.
+// sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c over n partials
+// (o[0..hd), m at hd, l at hd + 1, stride floats apart; m_c = -inf for a
+// chunk that saw nothing): 16 chunks' loads at a time, rescaled online, so
+// that one memory round trip covers up to 16 chunks
+__device__ __forceinline__ float merge_partials(const float* __restrict__ pp, size_t stride, int n, int hd, int d) {
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int c0 = 0; c0 < n; c0 += 16) {
+    float mv[16], lv[16], ov[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float* pc = pp + size_t(min(c0 + j, n - 1)) * stride;
+      mv[j] = pc[hd];
+      lv[j] = pc[hd + 1];
+      ov[j] = pc[d];
+    }
+    float bm = M;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (c0 + j < n) bm = fmaxf(bm, mv[j]);
+    if (bm == -INFINITY) continue;  // nothing seen yet
+    const float cs = M == -INFINITY ? 0.f : __expf(M - bm);
+    num *= cs;
+    den *= cs;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (c0 + j < n && mv[j] != -INFINITY) {
+        const float w = __expf(mv[j] - bm);
+        num += w * ov[j];
+        den += w * lv[j];
+      }
+    }
+    M = bm;
+  }
+  return den > 0.f ? num / den : 0.f;
+}
+
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
   const int h = int(blockIdx.x), d = int(threadIdx.x);
@@ -1754,18 +1790,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnParams p) {
   if (pos < 0 || pos >= p.max_seq) return;  // out was zeroed by attn_decode_kernel
   const float* part = p.part + size_t(h) * p.chunks * (HD + kAttnPad);
   const int used = int(pos / kAttnChunk) + 1;  // chunks past pos hold empty partials
-  float M = -INFINITY;
-#pragma unroll 8
-  for (int c = 0; c < used; ++c) M = fmaxf(M, part[size_t(c) * (HD + kAttnPad) + HD]);
-  float num = 0.f, den = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < used; ++c) {
-    const float* pc = part + size_t(c) * (HD + kAttnPad);
-    const float w = __expf(pc[HD] - M);  // chunk 0 holds position 0, so M is finite
-    num += pc[d] * w;
-    den += pc[HD + 1] * w;
-  }
-  p.out[size_t(h) * HD + d] = num / den;
+  p.out[size_t(h) * HD + d] = merge_partials(part, HD + kAttnPad, used, HD, d);
 }
 
 // ---------------------------------------------------------------------------
@@ -1985,8 +2010,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParam
 }
 
 // out[qi][h][d] = sum_c exp(m_c - M) o_c[d] / sum_c exp(m_c - M) l_c over
-// the chunks' partials, M the largest m_c (two passes, independent loads);
-// chunks where the query sees nothing hold m_c = -inf.  grid = (heads, N).
+// the chunks' partials (merge_partials); chunks where the query sees nothing
+// hold m_c = -inf.  grid = (heads, N).
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams p) {
   const int h = int(blockIdx.x), qi = int(blockIdx.y), d = int(threadIdx.x);
@@ -1997,19 +2022,7 @@ __global__ __launch_bounds__(HD) void attn_batch_combine_kernel(AttnBatchParams 
   }
   const size_t cstride = size_t(p.N) * (HD + 2);
   const float* pp = p.part + (size_t(h) * p.chunks * p.N + qi) * (HD + 2);
-  float M = -INFINITY;
-#pragma unroll 8
-  for (int c = 0; c < p.chunks; ++c) M = fmaxf(M, pp[size_t(c) * cstride + HD]);
-  float num = 0.f, den = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < p.chunks; ++c) {
-    const float* pc = pp + size_t(c) * cstride;
-    const float mc = pc[HD];
-    const float w = mc == -INFINITY ? 0.f : __expf(mc - M);
-    num += pc[d] * w;
-    den += pc[HD + 1] * w;
-  }
-  p.out[(size_t(qi) * p.heads + h) * HD + d] = num / den;
+  p.out[(size_t(qi) * p.heads + h) * HD + d] = merge_partials(pp, cstride, p.chunks, HD, d);
 }
 
 // ---------------------------------------------------------------------------
