@@ -108,6 +108,39 @@ def build_dummy_config(hf_config: Dict, littlebit_config: Dict) -> Dict:
     }
 
 
+def load_packed_checkpoint(model_path) -> Tuple[Dict[str, torch.Tensor], bool]:
+    """(state_dict, packed) from a LittleBit HF checkpoint directory: the
+    reference's _load_and_process_state_dict (quant_util.py:171-256) --
+    ``model.safetensors.index.json`` shards, else ``model.safetensors``, else
+    ``pytorch_model.bin`` -- except that the sign words stay packed: the
+    ``(prefix).(U|V|U_R|V_R)_(packed|shape)`` keys are kept as they are, for
+    :class:`~littlebit_amd.modules.LittleBitLinear` to take (its rank comes
+    from their shapes, which covers quant_util.py:259-297).  ``packed`` says
+    whether any ``_packed`` key was present.  A ``.bin`` file is read with
+    ``weights_only=True`` only (the reference retries without it; a file that
+    needs that is refused here)."""
+    from safetensors import safe_open
+
+    path = Path(model_path)
+    index, single, binf = path / "model.safetensors.index.json", path / "model.safetensors", path / "pytorch_model.bin"
+    state: Dict[str, torch.Tensor] = {}
+    if index.exists():
+        weight_map = json.loads(index.read_text(encoding="utf-8"))["weight_map"]
+        for shard in sorted(set(weight_map.values())):
+            with safe_open(str(path / shard), framework="pt", device="cpu") as f:
+                for k in f.keys():
+                    state[k] = f.get_tensor(k)
+    elif single.exists():
+        with safe_open(str(single), framework="pt", device="cpu") as f:
+            for k in f.keys():
+                state[k] = f.get_tensor(k)
+    elif binf.exists():
+        state = torch.load(str(binf), map_location="cpu", weights_only=True)
+    else:
+        raise FileNotFoundError(f"No model weights found in {path}")
+    return state, any(k.endswith("_packed") for k in state)
+
+
 def load_runtime_checkpoint(path, device: str = "cpu") -> Tuple[Dict[str, torch.Tensor], Optional[Dict]]:
     """(state_dict, runtime_config) from a converted runtime directory."""
     from safetensors.torch import load_file

@@ -171,3 +171,44 @@ def test_from_packed_runtime_branches_has_no_meta_tensors():
     m = LittleBitLinear.from_packed(K, N, brs)
     assert m.split_dim == 205 and m.split_dim_R == 37 and int(m._split_dim_final) == 205
     assert not any(t.is_meta for t in list(m.parameters()) + list(m.buffers()))
+
+
+def test_packed_checkpoint_reader_single_sharded_and_bin(tmp_path):
+    """load_packed_checkpoint reads model.safetensors, a sharded index, or a
+    pytorch_model.bin (weights_only), keeps the words packed, and a module
+    loads from it with the checkpoint's rank (quant_util.py:171-297)."""
+    import json
+    from safetensors.torch import save_file
+    from littlebit_amd.runtime import load_packed_checkpoint
+    rng = np.random.Generator(np.random.PCG64(4))
+    K, N = 96, 40
+    sd = {"layer." + k: v.contiguous() for k, v in _hf_packed_state("", rng, K, N, [11, 21]).items()}
+    sd["norm.weight"] = torch.ones(K)
+    one = tmp_path / "single"
+    one.mkdir()
+    save_file(sd, str(one / "model.safetensors"))
+    shard = tmp_path / "sharded"
+    shard.mkdir()
+    keys = sorted(sd)
+    a, b = keys[: len(keys) // 2], keys[len(keys) // 2:]
+    save_file({k: sd[k] for k in a}, str(shard / "model-00001-of-00002.safetensors"))
+    save_file({k: sd[k] for k in b}, str(shard / "model-00002-of-00002.safetensors"))
+    wm = {k: "model-00001-of-00002.safetensors" for k in a} | {k: "model-00002-of-00002.safetensors" for k in b}
+    (shard / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    binf = tmp_path / "bin"
+    binf.mkdir()
+    torch.save(sd, str(binf / "pytorch_model.bin"))
+    for d in (one, shard, binf):
+        state, packed = load_packed_checkpoint(d)
+        assert packed and sorted(state) == keys
+        for k in keys:
+            assert torch.equal(state[k], sd[k]), (d.name, k)
+        m = _convert(K, N, split_dim=8, residual=True)  # the skeleton's rank differs from the checkpoint's
+        m.load_state_dict({k[len("layer."):]: v for k, v in state.items() if k.startswith("layer.")}, strict=False)
+        assert m.split_dim == 11 and m.split_dim_R == 21
+    with pytest.raises(FileNotFoundError):
+        load_packed_checkpoint(tmp_path / "missing")
+    unpacked = tmp_path / "dense"
+    unpacked.mkdir()
+    save_file({"w": torch.zeros(2)}, str(unpacked / "model.safetensors"))
+    assert load_packed_checkpoint(unpacked)[1] is False
