@@ -1829,7 +1829,7 @@ struct AttnBatchParams {
 };
 
 template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_batch_kernel(AttnBatchParams p) {
+__global__ __launch_bounds__(kAttnThreads, 2) void attn_batch_kernel(AttnBatchParams p) {
   constexpr int DG = HD / 4;   // dims per lane group in the score MFMAs
   constexpr int NT = HD / 16;  // 16-dim tiles of O^T: tile 4a + b holds dims 64a + 4r + b, r < 16
   constexpr int NA = HD / 64;
