@@ -1,6 +1,6 @@
 """Benchmark of the LittleBitLinear forward on one MI355X.
 
-Workload (BASELINE config 2): the Llama-2-7B-shaped 0.1-BPW draft decode
+Workload: the Llama-2-7B-shaped 0.1-BPW draft decode
 step -- the 7 projections of each of 32 decoder layers at batch 1 (q, k, v, o
 4096->4096 rank 205; gate, up 4096->11008 rank 298; down 11008->4096 rank
 298), fp32 activations, random packed signs and |N(0,1)|+0.05 scales.  One
@@ -15,7 +15,7 @@ the 256 MB Infinity Cache.  The warm figure (one replica) is reported too.
 roofline = the call kind with the longest duration, one call = its two
 kernels (latent + expand) and the gap between them, timed with HIP events
 around a graph of 32 back-to-back calls of that kind; bytes per call from
-the BASELINE formula, summed over the call's projections.  cpu_baseline = the reference AVX2 kernel littlebit_linear
+sign words + scales + x read once + y written once, summed over the call's projections.  cpu_baseline = the reference AVX2 kernel littlebit_linear
 (oracle/_ref, built from the reference source) on the host cores, over a
 bounded number of whole steps.
 
@@ -47,7 +47,8 @@ MALL_BYTES = 256 << 20
 
 
 def proj_bytes(M, K, N, ranks, sx=4, sy=4):
-    """Algorithmic bytes of one forward (BASELINE formula)."""
+    """Algorithmic bytes of one forward: every branch's sign words and scales,
+    x read once and y written once (the latent vector stays on chip)."""
     b = 0
     for R in ranks:
         b += R * math.ceil(K / 32) * 4 + N * math.ceil(R / 32) * 4 + 4 * (K + R + N)
@@ -169,7 +170,7 @@ def call_duration_us(gen, dev, names, stream, count=32, steps=100, warmup=10):
     return calls[0], ms * 1000.0 / count
 
 
-# BASELINE config 4: Llama-3-8B-shaped prefill, draft 0.1 BPW + residual 0.9 BPW
+# Llama-3-8B-shaped prefill, draft 0.1 BPW + residual 0.9 BPW
 # per projection (ranks floor(bpw*K*N/(K+N))), M = 2048 bf16 tokens.
 PREFILL_M = 2048
 PREFILL_LAYER = [("qkv", [(4096, 4096, [204, 1843]), (4096, 1024, [81, 737]), (4096, 1024, [81, 737])]),

@@ -16,8 +16,8 @@ there from EAGLE):
 * :func:`evaluate_posterior_greedy` (:182-214) the longest candidate path
   that agrees with the target's argmax.
 
-The reference ships fixed presets of 9, 25 and 35 nodes
-asks for a 32-node tree of depth 5 with at most 4 children per node, which
+The reference ships fixed presets of 9, 25 and 35 nodes; the verify
+benchmark uses a 32-node tree of depth 5 with at most 4 children per node, which
 :func:`ranked_tree_choices` builds by a rule: the ``n`` most likely paths
 when the k-th ranked child is accepted with probability ``weights[k]``.
 """
@@ -61,7 +61,7 @@ def ranked_tree_choices(n_nodes: int, max_depth: int, max_branch: int,
 
 
 def config3_tree_choices() -> List[List[int]]:
-    """32 nodes, depth 5, at most 4 children per node."""
+    """32 nodes, depth 5, at most 4 children per node (the verify benchmark's tree)."""
     return ranked_tree_choices(32, 5, 4, weights=(0.72, 0.16, 0.07, 0.03))
 
 

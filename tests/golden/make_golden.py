@@ -17,8 +17,8 @@ forward_small.npz
     (correctly rounded sums) for the arithmetic.
 
 synthetic_digests.json
-    SHA-256 of the arrays the seeded generator draws for BASELINE configs 0
-    and 1 (numpy PCG64, seed 1000 + config index), so that a numpy change that
+    SHA-256 of the arrays the seeded generator draws for the single-layer
+    benchmark configurations 0 and 1 (numpy PCG64, seed 1000 + index), so that a numpy change that
     alters the stream is caught.
 
 Run:  python tests/golden/make_golden.py

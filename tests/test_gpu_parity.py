@@ -1,6 +1,6 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle.
 
-Bar (BASELINE north_star): sign unpacking bit-exact; forward
+Bar: sign unpacking bit-exact; forward
 max|y - y_ref| / max|y_ref| <= 1e-3 for fp32 outputs.  bf16 outputs add the
 rounding of the output itself (relative 2**-9 per element), so their bar is
 4e-3.  Inputs are the seeded generator's (numpy PCG64).
@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 TOL_F32 = 1e-3
 TOL_BF16_OUT = 4e-3
-TOL_BF16_PREFILL = 5e-3  # bf16 activations at M > 16: bf16 MFMA operands (BASELINE north_star)
+TOL_BF16_PREFILL = 5e-3  # bf16 activations at M > 16: bf16 MFMA operands
 
 
 def _dev_branch(b, dev):
