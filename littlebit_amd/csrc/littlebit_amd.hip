@@ -1865,10 +1865,10 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_batch_kernel(AttnBatchPa
   const bool qvalid = qi < N;
   float qv[DG];
   {
-    const float* qr = p.q + (size_t(min(qi, N - 1)) * p.heads + h) * HD + g * DG;
+    const float* qr = p.q + (size_t(min(qi, N - 1)) * p.heads + h) * HD + 4 * g;
 #pragma unroll
     for (int j = 0; j < DG / 4; ++j) {
-      const float4 f = *reinterpret_cast<const float4*>(qr + 4 * j);
+      const float4 f = *reinterpret_cast<const float4*>(qr + 16 * j);
       qv[4 * j] = f.x * p.scale;
       qv[4 * j + 1] = f.y * p.scale;
       qv[4 * j + 2] = f.z * p.scale;
@@ -1881,17 +1881,18 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_batch_kernel(AttnBatchPa
   f32x4 o[NT];
 #pragma unroll
   for (int dt = 0; dt < NT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // K row s0 + col, dims g*DG .. +DG (A of the score MFMAs); V rows
+  // K row s0 + col, dims 16 j + 4 g .. +4 for j < DG / 4 (A of the score
+  // MFMAs: the 4 lanes of a row read 64 contiguous bytes per load); V rows
   // s0 + 4g + i, dims 64a + 4col .. +4 (A of the value MFMAs); positions
   // past w1 read row w1 - 1 and are masked.  The next tile's rows load while
   // this tile computes.
   auto load_kv = [&](int s0, float (&kk)[DG], float4 (&vv)[4][NA]) {
     {
       const int t = min(s0 + col, w1 - 1);
-      const float* kr = (t < st ? kcache + size_t(t) * HD : knew + size_t(t - st) * nstride) + g * DG;
+      const float* kr = (t < st ? kcache + size_t(t) * HD : knew + size_t(t - st) * nstride) + 4 * g;
 #pragma unroll
       for (int j = 0; j < DG / 4; ++j) {
-        const float4 f = *reinterpret_cast<const float4*>(kr + 4 * j);
+        const float4 f = *reinterpret_cast<const float4*>(kr + 16 * j);
         kk[4 * j] = f.x;
         kk[4 * j + 1] = f.y;
         kk[4 * j + 2] = f.z;
