@@ -257,8 +257,8 @@ def prefill_bench(gen, dev, stream, steps=20, warmup=3):
 
 
 def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5):
-    """Config 3's verify linears: the 224 target projections (draft + residual
-    branch each) at M = 8, grouped as in the draft step, one HIP graph per
+    """The ~1.0-BPW target's verify linears: the 224 target projections (draft +
+    residual branch each) at M = 8 (a verify of 8 draft tokens), grouped as in the draft step, one HIP graph per
     pass, weights cold (2 replicas of 0.9 GB rotated)."""
     import torch
     reps = [DraftStep(gen, dev, layers, M=M, residual=True) for _ in range(2)]
@@ -273,10 +273,11 @@ def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5):
 
 
 def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, target=True):
-    """Config 2 draft tokens and config 3 verification on whole Llama-2-7B-shaped
-    models (random packed factors, |N|+0.05 scales; embedding and a bf16
-    lm_head N(0,1)): attention, norms and lm_head in PyTorch, linears on the
-    HIP kernels."""
+    """0.1-BPW draft tokens at KV length 512 and ~1.0-BPW target verification
+    (8 tokens, and a 33-token tree) at KV length 1024 on whole Llama-2-7B-shaped
+    models (random packed factors, |N|+0.05 scales; embedding and lm_head
+    N(0,1)): linears, attention and the Q4_0 lm_head on the HIP kernels,
+    norms inside the linear calls, one HIP graph per step."""
     import torch
     from littlebit_amd.decode import DecoderConfig, GPUDraftModel, GPUTargetModel
     from littlebit_amd.synthetic import LLAMA2_7B as C, synthetic_runtime_state
@@ -286,7 +287,7 @@ def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, tar
     ev = lambda: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))  # noqa: E731
     out = {}
     gen = torch.Generator().manual_seed(5)
-    # --- config 2: draft model, KV length 512 -------------------------------------
+    # --- draft model (0.1 BPW), KV length 512 -------------------------------------
     st = synthetic_runtime_state(cfg, C["draft_rank"], None, seed=1, device=dev)
     prompt = torch.randint(0, cfg.vocab_size, (1, kv_draft), generator=gen)
 
@@ -329,7 +330,7 @@ def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, tar
     torch.cuda.empty_cache()
     if not target:
         return out
-    # --- config 3: 1.0-BPW target (draft + residual branch per projection), KV length 1024
+    # --- 1.0-BPW target (draft + residual branch per projection), KV length 1024
     st = synthetic_runtime_state(cfg, C["draft_rank"], C["residual_rank"], seed=2, device=dev)
     target = GPUTargetModel(draft_state=st, config=cfg, device=dev, max_seq_len=kv_target + 64,
                             torch_dtype=torch.bfloat16)

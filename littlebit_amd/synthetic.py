@@ -99,7 +99,7 @@ def make_projection(seed: int, M: int, K: int, N: int, ranks: List[int],
 
 
 # Llama-2-7B shapes and the 0.1-BPW ranks of the draft, plus
-# the residual ranks that make the ~1.0-BPW target (config 3).
+# the residual ranks that make the ~1.0-BPW target.
 LLAMA2_7B = {
     "hidden": 4096,
     "intermediate": 11008,

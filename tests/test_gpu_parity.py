@@ -144,7 +144,7 @@ def test_bf16_in_bf16_out(gpu):
 
 
 def test_prefill_shape_small(gpu):
-    """bf16 activations at M > 16 take the bf16 GEMM path (config 4 shape, fewer tokens)."""
+    """bf16 activations at M > 16 take the bf16 GEMM path (a Llama-3-8B prefill shape, fewer tokens)."""
     K, N = 4096, 4096
     x, brs = _synthetic(1006, 256, K, N, [204, 1843])
     y, xu = _run(gpu, x, brs, x_dtype=torch.bfloat16, out_dtype=torch.float32)
