@@ -69,7 +69,12 @@ typedef struct lbk_branch {
  * optional fp32 residual [M, N] added to y (it may be y itself: the update
  * x += projection(...) of a decoder layer).  y may also share memory with
  * the call's input (the call then keeps its expand stage in one rank slice,
- * so that x is read before y is written). */
+ * so that x is read before y is written).  Where the rows of a call run as
+ * row chunks one after another (deterministic mode above 16 rows, or rows
+ * whose latent vectors do not fit at once), the chunks run first to last,
+ * or last to first, whichever reads every input row before an output row
+ * overlapping it is written; a call for which neither order does returns
+ * LBK_ERR_ARG. */
 typedef struct lbk_projection {
   const lbk_branch* branches;
   int n_branches;
@@ -182,16 +187,17 @@ int lbk_group_forward_ex(const lbk_projection* projs, int n_proj, int64_t M,
 /* lbk_group_forward_ex without a workspace argument: it calls no hipMalloc,
  * hipFree or allocating library routine, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * it).  No counterpart in the reference, whose CPU operators allocate their
- * outputs and scratch per call (patches/littlebit_cpu_optimized.cpp:642,
- * 652-660).  Its workspace is a device array of LBK_NOALLOC_SCRATCH_BYTES
+ * it).  It has no counterpart in the reference.  Its workspace is a device
+ * array of LBK_NOALLOC_SCRATCH_BYTES
  * that the library holds on each GPU it runs on until the process ends;
  * shapes whose smallest accepted workspace exceeds that return
  * LBK_ERR_WORKSPACE.  The calling thread's current device must be the
  * device of `stream`.  Every call on a GPU shares that GPU's array: calls
  * that overlap on one GPU (different streams, or threads without ordering)
  * race.  The first call on a device (and the first after a call that failed
- * with LBK_ERR_HIP) first zeroes the array with a kernel on `stream`. */
+ * with LBK_ERR_HIP) first zeroes the array with a kernel on `stream`; when
+ * `stream` is being captured, that kernel is part of the graph (it runs in
+ * every replay) and the next eager call zeroes the array again. */
 int lbk_group_forward_noalloc(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x,
                               int x_dtype, const lbk_input* input, int y_dtype, void* stream);
 
@@ -262,6 +268,19 @@ int lbk_unpack_signs(const int32_t* packed, int64_t rows, int64_t cols,
  * (quantization/utils/binary_packer.py:5-51) for inputs in {-1, +1}. */
 int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols,
                    int32_t* out, void* stream);
+
+/* Sign words [rows, words_per_row] -> the 2-bit layout of the reference's CPU
+ * runtime, out [rows, ceil(n_cols/4)] uint8, byte for byte what
+ * repack_signs_to_i2 (patches/littlebit_cpu_optimized.cpp:712-764, schema at
+ * :2340; called by cpu_draft_model.py:247-250) writes: column
+ * c = 128 b + 32 g + p is the field at bit shift 6 - 2 g of byte 32 b + p,
+ * 2 for +1 and 0 for -1.  As in the reference, a column whose byte index is
+ * >= ceil(n_cols/4) is dropped (the last block of a row when n_cols % 128 != 0)
+ * and fields no column fills are 0.  words_per_row must be at least
+ * ceil(n_cols/32) (LBK_ERR_ARG otherwise; the reference reads past the row). */
+int lbk_repack_signs_to_i2(const int32_t* packed, int64_t rows,
+                           int64_t words_per_row, int64_t n_cols,
+                           uint8_t* out, void* stream);
 
 /* Q4_0 quantisation of an lm_head weight w [rows][cols] fp32 (cols % 32 == 0),
  * as the reference's quantize_lm_head_q4 (patches/littlebit_cpu_optimized.cpp:

@@ -133,6 +133,7 @@ SIGNATURES = {
     ),
     "lbk_unpack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
     "lbk_pack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
+    "lbk_repack_signs_to_i2": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _VP]),
 }
 
 _lib = None

@@ -7,6 +7,10 @@ words are int32 (bit 31 is the sign bit).
 
 Tensors on a GPU are packed and unpacked by the HIP kernels of the library;
 CPU tensors (checkpoint load and save) by torch bit operations.
+
+``repack_signs_to_i2`` writes the 2-bit layout of the reference's CPU runtime
+(``littlebit_cpu_ops::repack_signs_to_i2``, patches/littlebit_cpu_optimized.cpp:
+712-764) from the words, on the GPU.
 """
 from __future__ import annotations
 
@@ -16,7 +20,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["binary_packer", "binary_unpacker", "words_per_row"]
+__all__ = ["binary_packer", "binary_unpacker", "repack_signs_to_i2", "words_per_row"]
 
 
 def words_per_row(cols: int) -> int:
@@ -89,3 +93,34 @@ def binary_unpacker(packed_tensor: torch.Tensor, original_shape: Tuple[int, int]
     bits = (words.unsqueeze(-1) >> torch.arange(32, dtype=torch.int64)) & 1
     bits = bits.reshape(n_rows, wpr * 32)[:, :n_cols]
     return (1 - 2 * bits).to(torch.int8)
+
+
+def repack_signs_to_i2(packed_signs: torch.Tensor, n_cols: int) -> torch.Tensor:
+    """Sign words [rows, words] -> uint8 [rows, ceil(n_cols/4)] in the
+    reference runtime's 2-bit layout, byte for byte as
+    ``littlebit_cpu_ops::repack_signs_to_i2`` (patch:712-764) writes it:
+    column ``128 b + 32 g + p`` is the field at bit shift ``6 - 2 g`` of byte
+    ``32 b + p``, 2 for +1 and 0 for -1; columns whose byte index reaches
+    ``ceil(n_cols/4)`` are dropped as the reference drops them.
+
+    The same checks as the reference (int32 words, :718) plus: the tensor is
+    on a GPU, 2-D, and holds at least ``ceil(n_cols/32)`` words per row.
+    """
+    if not isinstance(packed_signs, torch.Tensor) or not packed_signs.is_cuda:
+        raise RuntimeError("packed_signs must be a CUDA (HIP) tensor")
+    if packed_signs.dtype != torch.int32:
+        raise RuntimeError("packed_signs must be int32")
+    if packed_signs.dim() != 2:
+        raise RuntimeError(f"packed_signs must be 2-D, got {packed_signs.dim()} dimensions")
+    n_cols = int(n_cols)
+    if n_cols < 0:
+        raise RuntimeError(f"n_cols must be >= 0, got {n_cols}")
+    src = packed_signs.contiguous()
+    rows, wpr = src.shape
+    out = torch.empty((rows, (n_cols + 3) // 4), dtype=torch.uint8, device=src.device)
+    lib = _lib.load()
+    with torch.cuda.device(src.device):
+        rc = lib.lbk_repack_signs_to_i2(src.data_ptr(), rows, wpr, n_cols, out.data_ptr(),
+                                        _stream_handle(src.device))
+    _lib.check(rc, "repack_signs_to_i2")
+    return out

@@ -74,6 +74,7 @@ constexpr int kRowBlock = 64;                  // latent rows per latent_mfma bl
 constexpr int kMaxMfmaM = 16;                  // MFMA path handles M <= 16
 constexpr int kCounterSlots = 1024;            // counters at the workspace start
 constexpr float kTinyH = 1e-30f;               // |h1| below this: no h0 / h1 rescale (it could overflow)
+constexpr float kMaxHRatio = 1099511627776.f;  // 2^40: |h0 / h1| above this drops branch 1 (wide stage 2)
 constexpr size_t kCounterBytes = kCounterSlots * sizeof(uint32_t);
 
 // Encoding of s_waitcnt vmcnt(n) lgkmcnt(0) on gfx9 (expcnt left alone).
@@ -101,6 +102,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return uint16_t(u >> 16);
 }
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// Wide stage 2 keeps branch 1 of a column (rescaling acc by h0 / h1) unless
+// h1 is zero or denormal, or |h0 / h1| > 2^40 (the rescaled acc could
+// overflow, while h1's term is negligible there).
+__device__ __forceinline__ bool use_branch1(float h0, float h1) {
+  return fabsf(h1) >= kTinyH && fabsf(h0) <= fabsf(h1) * kMaxHRatio;
+}
 
 __device__ __forceinline__ void store_out(float* y, size_t i, float v) { y[i] = v; }
 __device__ __forceinline__ void store_out(uint16_t* y, size_t i, float v) { y[i] = f32_to_bf16(v); }
@@ -1621,9 +1629,10 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
 // +-g[k] instead of +-1: the 64 g values of a step are staged beside its
 // sign words, as bf16, in one of two 128-byte buffers (each wave fetches
 // them, wave 0 writes them), and each 16-k sub-step reads its 8 values.
-// In wide tiles (NJ = 4) with h given (the second branch of stage 2) it is
-// +-1 where the lane's column c has |h[c]| >= kTinyH and 0 elsewhere; both
-// branches run the same instantiation, so they share one stage ring.
+// In wide tiles (NJ = 4) with h given (the second branch of stage 2, h0 the
+// first branch's row scale) it is +-1 where the lane's column c keeps
+// branch 1 (use_branch1(h0[c], h[c])) and 0 elsewhere; both branches run
+// the same instantiation, so they share one stage ring.
 //
 // fill(f) issues the DMA of step f and the sign word (and g) of step f + 1.  Every
 // fill issues the same loads on every path; before step ks every wave waits
@@ -1640,7 +1649,8 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
                                               int m0, const uint32_t* __restrict__ W, int ldw, int ncols, int c0,
                                               int nks, f32x16 (&acc)[2][NJ], int tid,
                                               const float* __restrict__ g = nullptr, int kbase = 0,
-                                              const float* __restrict__ h = nullptr) {
+                                              const float* __restrict__ h = nullptr,
+                                              const float* __restrict__ h0 = nullptr) {
   static_assert(NJ == 2 || NJ == 4, "wave tiles of 64 x 64 or 64 x 128");
   static_assert(NJ == 2 || !GB, "wide tiles carry no g in the B operand");
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -1693,13 +1703,14 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
     }
   };
   // wide tiles: the +-1 pair of the lane's column in subtile j, or 0 where
-  // h is given and |h| < kTinyH (columns past ncols have zero sign words)
+  // h is given and the column drops branch 1 (columns past ncols have zero
+  // sign words)
   uint32_t hv[NJ];
   if constexpr (NJ == 4) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int n = min(c0 + 32 * NJ * wn + 32 * j + lr, ncols - 1);
-      hv[j] = !h || fabsf(h[n]) >= kTinyH ? 0x3F803F80u : 0u;
+      hv[j] = !h || use_branch1(h0[n], h[n]) ? 0x3F803F80u : 0u;
     }
   }
   // g of step st, lane's k (clamped: steps past the last are never read)
@@ -2038,8 +2049,10 @@ __global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
 // accumulators for both branches (two sets would not fit two blocks per CU):
 // acc = S0 after branch 0 (S_b = sum_r sU_b[n, r] * T_b[m, r]), each column's
 // acc times h0 / h1 in fp32, then branch 1 added: y = h1 * acc = h0 * S0 + h1
-// * S1, + bias (+ residual).  Where |h1| < kTinyH (zero or denormal, whose
-// ratio would overflow) branch 1's B operand is 0 and y = h0 * S0.
+// * S1, + bias (+ residual).  Where branch 1 is dropped (use_branch1: h1
+// zero, denormal or below 2^-40 |h0|, where h0 / h1 could overflow acc)
+// branch 1's B operand is 0 and y = h0 * S0; the term dropped is at most
+// 2^-40 of h0 times |S1 / S0|.
 template <typename YT>
 __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmParams p) {
   constexpr int NJ = 4, BN = 64 * NJ;
@@ -2069,7 +2082,7 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmPara
     const int n = min(c0 + 32 * NJ * wn + 32 * j + lr, P.N - 1);
     const float h0 = P.h[0][n];
     const float h1 = P.nb > 1 ? P.h[1][n] : 0.f;
-    const bool use1 = fabsf(h1) >= kTinyH;
+    const bool use1 = P.nb > 1 && use_branch1(h0, h1);
     f[j] = use1 ? h1 : h0;
     if (use1) {
       const float r = h0 / h1;
@@ -2079,7 +2092,7 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmPara
   }
   if (P.nb > 1)
     gemm_mainloop<false, false, NJ>(p.t + P.tbase[1], p.t_plane, P.RP[1], p.M, m0, P.U[1], P.RW[1], P.N, c0,
-                                    (P.RW[1] + 1) / 2, acc, tid, nullptr, 0, P.h[1]);
+                                    (P.RW[1] + 1) / 2, acc, tid, nullptr, 0, P.h[1], P.h[0]);
 
   YT* __restrict__ y = static_cast<YT*>(P.y);
 #pragma unroll
@@ -2127,6 +2140,47 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
     uint32_t word = 0;
     for (int j = 0; j < cn; ++j) word |= uint32_t(row[j] < 0) << j;
     out[i] = word;
+  }
+}
+
+// Sign words -> the 2-bit "i2" rows of the reference's CPU runtime
+// (repack_signs_to_i2_cpu, patches/littlebit_cpu_optimized.cpp:712-764), byte
+// for byte: out [rows][ob], ob = ceil(n_cols / 4).  Column c = 128 b + 32 g +
+// p is the field at bits 7-6 (g = 0) .. 1-0 (g = 3) of byte 32 b + p, 2 for +1
+// and 0 for -1; a column whose byte falls at or past ob is dropped and a field
+// with no column stays 0.  One thread per 4 output bytes j0 .. j0 + 3 (one b,
+// p .. p + 3): per g it inverts bits p .. p + 3 of word 4 b + g (+1 -> 1),
+// masks the columns past n_cols and spreads the 4 bits to bit 7 - 2 g of the
+// 4 bytes.  The word index 4 b + g = c / 32 of a column c < n_cols is below
+// ceil(n_cols / 32) <= wpr (checked by the host).
+__global__ __launch_bounds__(kBlock) void repack_i2_kernel(const uint32_t* __restrict__ packed, int64_t rows,
+                                                           int64_t wpr, int64_t n_cols, int64_t ob, int dword_rows,
+                                                           uint8_t* __restrict__ out) {
+  const int64_t nq = (ob + 3) / 4;
+  const int64_t total = rows * nq;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += int64_t(gridDim.x) * kBlock) {
+    const int64_t r = i / nq;
+    const int64_t j0 = 4 * (i - r * nq);
+    const int64_t b = j0 >> 5;
+    const int p = int(j0 & 31);
+    uint32_t d = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t c0 = 128 * b + 32 * g + p;  // column of byte j0's field g
+      if (c0 < n_cols) {
+        uint32_t nib = (~packed[r * wpr + 4 * b + g] >> p) & 0xfu;
+        if (n_cols - c0 < 4) nib &= (1u << (n_cols - c0)) - 1u;
+        const uint32_t spread = (nib & 1u) | ((nib & 2u) << 7) | ((nib & 4u) << 14) | ((nib & 8u) << 21);
+        d |= spread << (7 - 2 * g);
+      }
+    }
+    uint8_t* dst = out + r * ob + j0;
+    if (dword_rows) {
+      *reinterpret_cast<uint32_t*>(dst) = d;
+    } else {
+      const int nbytes = int(ob - j0 < 4 ? ob - j0 : 4);
+      for (int e = 0; e < nbytes; ++e) dst[e] = uint8_t(d >> (8 * e));
+    }
   }
 }
 
@@ -3008,6 +3062,9 @@ struct Plan {
   int ks;        // expand_mfma_kernel rank slices (grid.y)
   bool allow_ks; // rank slices were allowed (chunks plan with the same rule)
   int chunk;     // > 0: rows per decode-path call, the call runs over chunks of rows
+  bool det;      // deterministic mode, read once when the call is planned
+  bool seq;      // chunk > 0: one launch pair per chunk, one chunk after another
+  bool reverse;  // seq: the chunks run last to first (an output overlapping the input)
   size_t lds1, lds2;
   size_t ws_total;  // workspace the fastest form of the call uses
   size_t ws_min;    // workspace it needs (GEMM path: without the stream-K partial tiles)
@@ -3202,9 +3259,10 @@ ExpandChoice expand_shape(const ProjDesc* pd, int np, int mt, bool allow_ks, int
 // in deterministic mode).
 // nchunks: row chunks of this plan's rows that run side by side in one
 // launch pair (the expand kernel's blocks multiply by it).
-Plan plan_one(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks, int nchunks = 1) {
+Plan plan_one(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks, bool det, int nchunks = 1) {
   Plan pl{};
   pl.allow_ks = allow_ks;
+  pl.det = det;
   int64_t nrb = 0;
   pl.mt = mtile(M);
   bool small_u = false;  // a U matrix of fewer than 4 words: no 16-byte sign loads
@@ -3236,7 +3294,7 @@ Plan plan_one(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks, i
     pl.splits = ex.splits;
     pl.ks = ex.ks;
     pl.ws_total = pl.ws_min = kTOffset + kTBytes;
-    if (g_deterministic.load() && pl.nkc > 1)
+    if (det && pl.nkc > 1)
       pl.ws_total = pl.ws_min = kTOffset + kTBytes + align256(det_part_floats(pd, np, M, pl.nkc) * sizeof(float));
   } else {
     pl.ws_min = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
@@ -3268,15 +3326,16 @@ bool t_fits(const ProjDesc* pd, int np, int64_t M) {
 // calls), else 16 (one launch pair per chunk: fewer pairs).  Side by side,
 // 9-16 rows also go as 8-row chunks rather than one 16-row pass (measured 6-11
 // % faster at 9, 12 and 16 rows over the draft and target calls).
-Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks) {
-  const Plan pl = plan_one(pd, np, M, K, allow_ks);
-  const bool side_by_side = !g_deterministic.load() && t_fits(pd, np, M);
+Plan make_plan(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks, bool det) {
+  const Plan pl = plan_one(pd, np, M, K, allow_ks, det);
+  const bool side_by_side = !det && t_fits(pd, np, M);
   if ((!pl.mfma || (M > 8 && side_by_side)) && M > 1 && M <= kMaxChunkedM) {
     for (int64_t c : {side_by_side ? int64_t(8) : int64_t(16), side_by_side ? int64_t(16) : int64_t(8)}) {
       if (c >= M) continue;
-      Plan pc = plan_one(pd, np, c, K, allow_ks, side_by_side ? int(ceil_div(M, c)) : 1);
+      Plan pc = plan_one(pd, np, c, K, allow_ks, det, side_by_side ? int(ceil_div(M, c)) : 1);
       if (pc.mfma) {
         pc.chunk = int(c);
+        pc.seq = !side_by_side;
         return pc;
       }
     }
@@ -3422,7 +3481,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.sync = reinterpret_cast<uint32_t*>(ws);
   p.t2 = reinterpret_cast<float*>(ws + kTOffset);
   // the plan sized the workspace for the partials when the mode was on
-  const bool det = g_deterministic.load() && pl.nkc > 1 && pl.ws_min > kTOffset + kTBytes;
+  const bool det = pl.det && pl.nkc > 1 && pl.ws_min > kTOffset + kTBytes;
   p.part = det ? reinterpret_cast<float*>(ws + kTOffset + kTBytes) : nullptr;
   p.det_cnt = det ? reinterpret_cast<uint32_t*>(ws + kDetCntOffset) : nullptr;
 
@@ -3579,8 +3638,8 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
 // has set y = bias + residual, so y must be fp32, the mode not deterministic,
 // and no y may overlap what the latent kernel reads (x, x1).
 bool slices_allowed(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, int x_dtype,
-                    const InputDesc& in, int y_dtype) {
-  if (y_dtype != LBK_F32 || g_deterministic.load()) return false;
+                    const InputDesc& in, int y_dtype, bool det) {
+  if (y_dtype != LBK_F32 || det) return false;
   const size_t xb = x_dtype == LBK_F32 ? 4 : 2;
   size_t xbytes = size_t(M) * size_t(K) * xb;
   if (in.kind == LBK_INPUT_ATTN_MERGE)  // partials [K / head_dim][chunks][head_dim + 4] fp32
@@ -3596,9 +3655,48 @@ bool slices_allowed(const ProjDesc* pd, int np, int64_t M, int64_t K, const void
 // Workspace a call of these shapes needs whatever its output dtype and
 // buffers (with or without rank slices).
 size_t query_workspace(const ProjDesc* pd, int np, int64_t M, int64_t K) {
-  const Plan a = make_plan(pd, np, M, K, false);
-  if (g_deterministic.load()) return a.ws_total;
-  return std::max(a.ws_total, make_plan(pd, np, M, K, true).ws_total);
+  const bool det = g_deterministic.load() != 0;
+  const Plan a = make_plan(pd, np, M, K, false, det);
+  if (det) return a.ws_total;
+  return std::max(a.ws_total, make_plan(pd, np, M, K, true, det).ws_total);
+}
+
+// Chunks run one after another (Plan::seq): chunk c reads rows [c * ch,
+// (c + 1) * ch) of x, x1 and each residual, then writes the same rows of
+// each y.  An output overlapping an input row that a later chunk still has
+// to read would change that chunk's input, so the chunks run in an order
+// in which no chunk's output rows overlap the input rows of any chunk after
+// it: first to last, else last to first (e.g. y at x's address with wider
+// rows than x), else the call is refused.
+bool chunk_order_safe(const ProjDesc* pd, int np, int64_t M, int64_t K, int64_t ch, const void* x, size_t xb,
+                      const void* x1, int y_dtype, bool reverse) {
+  const size_t yb = y_dtype == LBK_F32 ? 4 : 2;
+  const int64_t nc = ceil_div(M, ch);
+  auto rows = [&](int64_t c, int64_t& m0, int64_t& mc) {
+    m0 = c * ch;
+    mc = std::min<int64_t>(ch, M - m0);
+  };
+  for (int64_t i = 0; i < nc; ++i) {
+    int64_t m0, mc;
+    rows(i, m0, mc);
+    for (int q = 0; q < np; ++q) {
+      const char* y = static_cast<const char*>(pd[q].y) + size_t(m0) * size_t(pd[q].N) * yb;
+      const size_t ybytes = size_t(mc) * size_t(pd[q].N) * yb;
+      for (int64_t j = reverse ? 0 : i + 1; j < (reverse ? i : nc); ++j) {
+        int64_t n0, nn;
+        rows(j, n0, nn);
+        const size_t xo = size_t(n0) * size_t(K) * xb, xn = size_t(nn) * size_t(K) * xb;
+        if (overlaps(y, ybytes, static_cast<const char*>(x) + xo, xn)) return false;
+        if (x1 && overlaps(y, ybytes, static_cast<const char*>(x1) + xo, xn)) return false;
+        for (int r = 0; r < np; ++r) {
+          if (!pd[r].res) continue;
+          const float* res = pd[r].res + size_t(n0) * size_t(pd[r].N);
+          if (overlaps(y, ybytes, res, size_t(nn) * size_t(pd[r].N) * 4)) return false;
+        }
+      }
+    }
+  }
+  return true;
 }
 
 // Validation and plan of a group call, without touching the device; M == 0
@@ -3648,7 +3746,19 @@ int prepare_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
   if (!x) return set_error(LBK_ERR_ARG, "x is NULL");
   for (int q = 0; q < np; ++q)
     if (!pd[q].y) return set_error(LBK_ERR_ARG, "projection %d: y is NULL", q);
-  pl = make_plan(pd, np, M, K, slices_allowed(pd, np, M, K, x, x_dtype, in, y_dtype));
+  const bool det = g_deterministic.load() != 0;
+  pl = make_plan(pd, np, M, K, slices_allowed(pd, np, M, K, x, x_dtype, in, y_dtype, det), det);
+  if (pl.chunk > 0 && pl.seq) {
+    const size_t xb = x_dtype == LBK_F32 ? 4 : 2;
+    if (!chunk_order_safe(pd, np, M, K, pl.chunk, x, xb, in.x1, y_dtype, false)) {
+      if (!chunk_order_safe(pd, np, M, K, pl.chunk, x, xb, in.x1, y_dtype, true))
+        return set_error(LBK_ERR_ARG,
+                         "an output overlaps input rows of other row chunks (%lld rows run as chunks of %d): "
+                         "pass an output that does not share memory with the input",
+                         (long long)M, pl.chunk);
+      pl.reverse = true;
+    }
+  }
   if (in.kind == LBK_INPUT_ATTN_MERGE && (!pl.mfma || pl.chunk > 0))
     return set_error(LBK_ERR_ARG, "LBK_INPUT_ATTN_MERGE: the projections have no one-row decode plan");
   return LBK_OK;
@@ -3662,7 +3772,7 @@ int run_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, i
   if (!workspace || workspace_bytes < pl.ws_min)
     return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pl.ws_min, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (pl.chunk > 0 && !g_deterministic.load() && t_fits(pd, np, M)) {
+  if (pl.chunk > 0 && !pl.seq) {
     // every chunk's t fits the latent half: the chunks run side by side in
     // one launch pair (each block takes one chunk's rows)
     return forward_mfma(pd, np, pl, M, K, x, x_dtype, in, y_dtype, workspace, s);
@@ -3671,7 +3781,9 @@ int run_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, i
     // one launch pair per chunk (deterministic mode sizes its partials for
     // one chunk; or the rows' t does not fit the latent half at once)
     const size_t xb = x_dtype == LBK_F32 ? 4 : 2, yb = y_dtype == LBK_F32 ? 4 : 2;
-    for (int64_t m0 = 0; m0 < M; m0 += pl.chunk) {
+    const int64_t nc = ceil_div(M, pl.chunk);
+    for (int64_t i = 0; i < nc; ++i) {
+      const int64_t m0 = (pl.reverse ? nc - 1 - i : i) * pl.chunk;
       const int64_t mc = std::min<int64_t>(pl.chunk, M - m0);
       ProjDesc pc[kMaxProj];
       for (int q = 0; q < np; ++q) {
@@ -3681,8 +3793,10 @@ int run_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* x, i
       }
       InputDesc ic = in;
       if (ic.x1) ic.x1 = static_cast<const char*>(in.x1) + size_t(m0) * size_t(K) * xb;
-      const Plan pm = plan_one(pc, np, mc, K, pl.allow_ks);
+      const Plan pm = plan_one(pc, np, mc, K, pl.allow_ks, pl.det);
       if (!pm.mfma) return set_error(LBK_ERR_ARG, "a chunk of %lld rows has no decode-path plan", (long long)mc);
+      if (pm.ws_min > workspace_bytes)
+        return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", pm.ws_min, workspace_bytes);
       rc = forward_mfma(pc, np, pm, mc, K, static_cast<const char*>(x) + size_t(m0) * size_t(K) * xb, x_dtype, ic,
                         y_dtype, workspace, s);
       if (rc != LBK_OK) return rc;
@@ -3747,12 +3861,18 @@ int device_scratch(hipStream_t s, void** out) {
     slot.ptr = ptr;
   }
   if (!slot.clean) {
+    // A clear enqueued while `s` is being captured runs in every replay of
+    // the graph and never now: the array stays marked unclean, so the next
+    // eager call clears it again (a capture query that fails counts as a
+    // capture).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
     const int64_t n16 = int64_t(kScratchBytes / 16);
     hipLaunchKernelGGL(clear_kernel, dim3(unsigned(std::min<int64_t>(ceil_div(n16, kBlock), 2048))), dim3(kBlock), 0,
                        s, static_cast<u32x4*>(slot.ptr), n16);
     const int rc = check_launch("clear_kernel");
     if (rc != LBK_OK) return rc;
-    slot.clean = true;
+    if (!capturing) slot.clean = true;
   }
   *out = slot.ptr;
   return LBK_OK;
@@ -3885,6 +4005,25 @@ int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols, int32_t* out
   hipLaunchKernelGGL(pack_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), signs,
                      rows, cols, wpr, reinterpret_cast<uint32_t*>(out));
   return check_launch("pack_kernel");
+}
+
+int lbk_repack_signs_to_i2(const int32_t* packed, int64_t rows, int64_t words_per_row, int64_t n_cols, uint8_t* out,
+                           void* stream) {
+  g_last_error[0] = '\0';
+  if (rows < 0 || n_cols < 0 || words_per_row < 0) return set_error(LBK_ERR_ARG, "negative shape");
+  if (words_per_row < ceil_div(n_cols, 32))
+    return set_error(LBK_ERR_ARG, "n_cols (%lld) needs %lld sign words per row, packed_signs has %lld",
+                     (long long)n_cols, (long long)ceil_div(n_cols, 32), (long long)words_per_row);
+  const int64_t ob = ceil_div(n_cols, 4);
+  if (rows == 0 || ob == 0) return LBK_OK;
+  if (!packed || !out) return set_error(LBK_ERR_ARG, "NULL pointer");
+  const int64_t total = rows * ceil_div(ob, 4);
+  const int64_t blocks = ceil_div(total, kBlock) < 65536 ? ceil_div(total, kBlock) : 65536;
+  // whole dwords when every row starts and ends on one
+  const int dword_rows = (ob % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 3u) == 0) ? 1 : 0;
+  hipLaunchKernelGGL(repack_i2_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint32_t*>(packed), rows, words_per_row, n_cols, ob, dword_rows, out);
+  return check_launch("repack_i2_kernel");
 }
 
 size_t lbk_attention_partial_bytes(int heads, int max_seq, int head_dim) {

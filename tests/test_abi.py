@@ -222,6 +222,12 @@ def test_pack_unpack_argument_errors():
     assert lib.lbk_unpack_signs(None, -1, 4, None, None) == L.LBK_ERR_ARG
     assert lib.lbk_pack_signs(None, 2, -4, None, None) == L.LBK_ERR_ARG
     assert lib.lbk_unpack_signs(None, 0, 4, None, None) == L.LBK_OK  # empty: nothing to do
+    assert lib.lbk_repack_signs_to_i2(None, 2, 2, -1, None, None) == L.LBK_ERR_ARG
+    assert lib.lbk_repack_signs_to_i2(None, 2, 2, 65, None, None) == L.LBK_ERR_ARG  # 65 columns need 3 words
+    assert "3 sign words" in L.last_error()
+    assert lib.lbk_repack_signs_to_i2(None, 2, 3, 65, None, None) == L.LBK_ERR_ARG  # NULL pointers
+    assert lib.lbk_repack_signs_to_i2(None, 0, 3, 65, None, None) == L.LBK_OK  # no rows
+    assert lib.lbk_repack_signs_to_i2(None, 4, 0, 0, None, None) == L.LBK_OK  # no columns
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
@@ -253,3 +259,31 @@ def test_q4_head_argument_errors():
     assert fx(0x1000, 0x1000, 100, 64, None, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
     assert fx(0x1000, 0x1000, 100, 64, 0x1004, None, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
     assert fx(0x1000, 0x1000, 100, 64, 0x1000, 0x1008, 0.0, None, 0x1000, 0x1000, 1 << 20, None) == L.LBK_ERR_ARG
+
+
+def test_output_overlapping_later_chunks_is_refused():
+    """Rows that run as row chunks one after another (48 rows of three
+    target-shaped projections: their latent vectors do not fit at once): an
+    output over the input rows of the next chunk (projection 0, one chunk
+    down) is safe only last to first, one over the previous chunk's rows
+    (projection 1, one chunk up) only first to last; with both in one call no
+    order is safe and the call is refused before any launch."""
+    import littlebit_amd._lib as L
+    lib = L.load()
+    K, N, M = 4096, 2048, 48          # fp32 y rows of N = bf16 x rows of K: 8 KiB each
+    brs = [(L.LbkBranch * 2)() for _ in range(3)]
+    for b in brs:
+        for i, r in enumerate((205, 1843)):
+            b[i].v_sign = b[i].u_sign = b[i].v2 = b[i].mid = b[i].u1 = 0x1000
+            b[i].rank = r
+    arr = (L.LbkProjection * 3)()
+    X, row, chunk = 0x40000000, 2 * K, 16
+    ys = [X + chunk * row, X - chunk * row, 0x80000000]
+    for i in range(3):
+        arr[i].branches = ctypes.cast(brs[i], ctypes.POINTER(L.LbkBranch))
+        arr[i].n_branches = 2
+        arr[i].out_features = N
+        arr[i].y = ys[i]
+    rc = lib.lbk_group_forward_ex(arr, 3, M, K, X, L.LBK_BF16, None, L.LBK_F32, 0x1000, 1 << 30, None)
+    assert rc == L.LBK_ERR_ARG
+    assert "overlaps input rows of other row chunks" in L.last_error()

@@ -97,3 +97,37 @@ def test_wide_tiles_group_bias_residual(gpu, out_dtype):
         err = O.rel_err(outs[i].float().cpu().numpy()[rows], ref)
         print(f"[wide] group proj {i} out={out_dtype} rel_err={err:.3e}", flush=True)
         assert err <= TOL_BF16_PREFILL
+
+
+def test_wide_tiles_large_scale_ratio_with_large_inputs(gpu):
+    """Columns with |h0 / h1| far beyond 2^40 (h1 = 1e-29, h0 = 1e3) on inputs
+    of magnitude 1e6: rescaling acc by h0 / h1 would overflow fp32 there, so
+    branch 1 is dropped (its term is below 2^-40 of branch 0's scale); columns
+    with |h0 / h1| just under 2^40 keep the rescale.  Every output finite and
+    within the bar against the oracle."""
+    from littlebit_amd import LittleBitProjection
+    from littlebit_amd.synthetic import make_branch
+    M, K, N = 1024, 256, 16384
+    rng = np.random.Generator(np.random.PCG64(9150))
+    brs = [make_branch(rng, K, R, N, direct_words=True).as_dict() for R in (40, 300)]
+    h0 = np.asarray(brs[0]["h"], np.float32).copy()
+    h1 = np.asarray(brs[1]["h"], np.float32).copy()
+    h1[0:64] = np.float32(1e-29)
+    h0[0:64] = np.float32(1e3)
+    h1[64:128] = h0[64:128] * np.float32(2.0 ** -39)   # ratio 2^39: rescaled
+    h1[128:192] = -np.float32(1e-29)
+    h0[128:192] = -np.float32(1e3)
+    brs[0]["h"], brs[1]["h"] = h0, h1
+    proj = LittleBitProjection([_dev_branch(b, gpu) for b in brs])
+    x = torch.from_numpy((rng.standard_normal((M, K)) * 1e6).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    y = proj.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    yc = y.cpu().numpy()
+    assert np.isfinite(yc).all()
+    rows = _rows(M, 9151)
+    ref = O.littlebit_forward(x.float().cpu().numpy()[rows], brs, K, N)
+    yr = yc[rows]
+    for lo, hi in [(0, 64), (64, 128), (128, 192), (192, N)]:
+        e = O.rel_err(yr[:, lo:hi], ref[:, lo:hi])
+        print(f"[wide] large ratio columns {lo}-{hi} rel_err={e:.3e}", flush=True)
+        assert e <= TOL_BF16_PREFILL, (lo, hi, e)

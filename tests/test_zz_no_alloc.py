@@ -104,3 +104,55 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(gpu):
     ya, yb, host, xs = _both(gpu, 2, 512, [(96, [45, 7])], 7600)
     assert O.rel_err(ya[0], yb[0]) <= 1e-5
     assert O.rel_err(ya[0], O.littlebit_forward(xs, host[0], 512, 96)) <= TOL_F32
+
+
+def test_noalloc_captured_and_replayed_between_eager_calls(gpu):
+    """A noalloc call captured in a graph and replayed four times, with eager
+    noalloc calls of another shape on the same scratch between the replays
+    (the replays and the eager calls hand the latent buffer on to each
+    other); every replay and every eager call against the oracle."""
+    import littlebit_amd._lib as L
+    lib = L.load()
+    K, M, specs = 4096, 8, [(4096, [205, 1843])]
+    x, host, projs = _projections(7700, M, K, specs, gpu)
+    tx = torch.from_numpy(x).to(gpu)
+    y = torch.zeros((M, 4096), device=gpu)
+    arr = _array(projs, [y])
+    ref = O.littlebit_forward(x, host[0], K, 4096)
+    # the eager shape: one row of a draft gate/up-like projection
+    xe, host_e, projs_e = _projections(7800, 1, K, [(11008, [298])], gpu)
+    txe = torch.from_numpy(xe).to(gpu)
+    ye = torch.zeros((1, 11008), device=gpu)
+    arr_e = _array(projs_e, [ye])
+    ref_e = O.littlebit_forward(xe, host_e[0], K, 11008)
+
+    def eager():
+        rc = lib.lbk_group_forward_noalloc(arr_e, 1, 1, K, txe.data_ptr(), L.LBK_F32, None, L.LBK_F32,
+                                           torch.cuda.current_stream(gpu).cuda_stream)
+        L.check(rc, "lbk_group_forward_noalloc (eager)")
+        torch.cuda.synchronize()
+        assert O.rel_err(ye.cpu().numpy(), ref_e) <= TOL_F32
+
+    eager()  # the scratch is set up and cleared before the capture
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        # warm the call on the capture stream once, eagerly
+        L.check(lib.lbk_group_forward_noalloc(arr, 1, M, K, tx.data_ptr(), L.LBK_F32, None, L.LBK_F32,
+                                              side.cuda_stream), "lbk_group_forward_noalloc (warm)")
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    print("[noalloc] capturing M=8 target q shape", flush=True)
+    with torch.cuda.graph(graph):
+        rc = lib.lbk_group_forward_noalloc(arr, 1, M, K, tx.data_ptr(), L.LBK_F32, None, L.LBK_F32,
+                                           torch.cuda.current_stream(gpu).cuda_stream)
+    L.check(rc, "lbk_group_forward_noalloc (captured)")
+    for rep in range(4):
+        y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        err = O.rel_err(y.cpu().numpy(), ref)
+        print(f"[noalloc] replay {rep}: rel_err={err:.2e}", flush=True)
+        assert err <= TOL_F32, (rep, err)
+        eager()
