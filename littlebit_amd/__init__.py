@@ -9,10 +9,11 @@ Public surface:
   * :class:`LittleBitProjectionGroup` -- projections sharing one input
     (q/k/v, gate/up) in the launches of one
   * :func:`binary_packer` / :func:`binary_unpacker` -- the reference word format
+  * :func:`repack_signs_to_i2` -- the reference CPU runtime's 2-bit sign rows
   * :func:`set_deterministic` / :func:`deterministic` -- bit-for-bit repeatable
     decode-path calls (fixed-order split-K sums)
 """
-from .binary_packer import binary_packer, binary_unpacker, words_per_row
+from .binary_packer import binary_packer, binary_unpacker, repack_signs_to_i2, words_per_row
 from .ops import (LittleBitBranch, LittleBitProjection, LittleBitProjectionGroup, deterministic, littlebit_forward,
                   littlebit_linear, set_deterministic)
 from .modules import LittleBitLinear, sign_pm1
@@ -26,6 +27,7 @@ __all__ = [
     "littlebit_linear",
     "binary_packer",
     "binary_unpacker",
+    "repack_signs_to_i2",
     "words_per_row",
     "sign_pm1",
     "set_deterministic",

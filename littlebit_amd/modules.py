@@ -82,39 +82,42 @@ class LittleBitLinear(nn.Linear):
         self._proj: Optional[LittleBitProjection] = None
 
     @staticmethod
+    def _bits_per_weight(a: int, b: int, rank: int, residual: bool) -> float:
+        """What a rank-``rank`` factorisation of an a x b weight costs per weight
+        (the accounting of littlebit.py:83-93): per branch, one sign per entry
+        of U and V plus 16 bits per latent entry (rank * (a + b + 16)), and
+        16 bits per input and output scale (16 * (a + b)); the residual form
+        holds two branches."""
+        if a * b == 0:
+            return float("inf")
+        branches = 2 if residual else 1
+        return branches * (rank * (a + b + 16) + 16 * (a + b)) / (a * b)
+
+    @staticmethod
     def _estimate_split_dim(a, b, eff_bit_target, residual) -> Optional[float]:
-        """Float split_dim for a bit budget (littlebit.py:50-63)."""
+        """The (fractional) rank at which _bits_per_weight meets
+        ``eff_bit_target``, solved from its linear form (littlebit.py:50-63);
+        None without a target or for an empty weight."""
         if eff_bit_target is None or a * b == 0:
             return None
-        base = a + b + 16
-        if residual:
-            numerator = a * b * eff_bit_target - 32 * (a + b)
-            denominator = 2 * base
-        else:
-            numerator = a * b * eff_bit_target - 16 * (a + b)
-            denominator = base
-        return numerator / denominator if denominator else None
+        branches = 2 if residual else 1
+        per_rank = branches * (a + b + 16)
+        fixed = branches * 16 * (a + b)
+        return (a * b * eff_bit_target - fixed) / per_rank if per_rank else None
 
     @staticmethod
     def _finalize_split_dim(split_float, split_default, min_split_dim) -> int:
-        """Round down to a multiple of 8, at least min_split_dim (littlebit.py:65-81)."""
-        cand = split_float if split_float is not None else split_default
-        cand = int(cand) if cand is not None else 0
-        cand = (cand // 8) * 8
-        if cand == 0:
-            cand = min_split_dim
-        return max(cand, min_split_dim)
+        """The estimate (the default without one), truncated to an integer and
+        rounded down to a multiple of 8; zero or anything below
+        ``min_split_dim`` gives ``min_split_dim`` (littlebit.py:65-81)."""
+        raw = split_default if split_float is None else split_float
+        rank = 8 * (int(raw or 0) // 8)
+        return max(rank or min_split_dim, min_split_dim)
 
     @staticmethod
     def _compute_eff_bits(a: int, b: int, s: int, residual: bool) -> float:
-        """Bits per weight of the factorisation (littlebit.py:83-93)."""
-        if a * b == 0:
-            return float("inf")
-        if residual:
-            num = s * 2 * (a + b + 16) + 32 * (a + b)
-        else:
-            num = s * (a + b + 16) + 16 * (a + b)
-        return num / (a * b)
+        """Bits per weight of the rank-s factorisation (littlebit.py:83-93)."""
+        return LittleBitLinear._bits_per_weight(a, b, s, residual)
 
     def _initialize_empty_parameters(self):
         """Meta-device placeholders with the reference names (littlebit.py:144-173)."""

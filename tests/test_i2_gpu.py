@@ -27,8 +27,8 @@ def _words(rng, rows, n, extra=0):
 
 
 def _gpu_repack(gpu, w, n):
-    from littlebit_amd import binary_packer as bp
-    out = bp.repack_signs_to_i2(torch.from_numpy(np.ascontiguousarray(w)).to(gpu), n)
+    from littlebit_amd import repack_signs_to_i2
+    out = repack_signs_to_i2(torch.from_numpy(np.ascontiguousarray(w)).to(gpu), n)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -70,14 +70,14 @@ def test_repack_tails_and_strides(gpu, rows, n, extra):
 
 
 def test_repack_empty_and_errors(gpu):
-    from littlebit_amd import binary_packer as bp
+    from littlebit_amd import repack_signs_to_i2
     z = torch.zeros((0, 3), dtype=torch.int32, device=gpu)
-    assert tuple(bp.repack_signs_to_i2(z, 70).shape) == (0, 18)
+    assert tuple(repack_signs_to_i2(z, 70).shape) == (0, 18)
     z = torch.zeros((3, 1), dtype=torch.int32, device=gpu)
-    assert tuple(bp.repack_signs_to_i2(z, 0).shape) == (3, 0)
+    assert tuple(repack_signs_to_i2(z, 0).shape) == (3, 0)
     with pytest.raises(RuntimeError, match="sign words"):
-        bp.repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int32, device=gpu), 65)
+        repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int32, device=gpu), 65)
     with pytest.raises(RuntimeError, match="int32"):
-        bp.repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int64, device=gpu), 40)
+        repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int64, device=gpu), 40)
     with pytest.raises(RuntimeError, match="CUDA"):
-        bp.repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int32), 40)
+        repack_signs_to_i2(torch.zeros((2, 2), dtype=torch.int32), 40)
