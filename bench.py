@@ -576,6 +576,23 @@ def cpu_baseline(layers, budget_s=12.0):
                        f"threads_4: the same with 4 threads, {steps4} steps in {el4:.1f} s")}
 
 
+def stage_handoff(stages: int = 64):
+    """One dependent stage as a kernel boundary (launches in a graph) and as
+    a grid-wide handoff inside one launch (agent-scope stores, non-returning
+    counter adds, polled counters; littlebit_amd/csrc/handoff_probe.hip), in
+    us per stage.  Run as a child process (the probe is its own program)."""
+    import subprocess
+    from littlebit_amd.build import PROBE_PATH
+    if not PROBE_PATH.exists():
+        return {"error": f"{PROBE_PATH} not built (python -m littlebit_amd.build)"}
+    proc = subprocess.run([str(PROBE_PATH), str(stages)], capture_output=True, text=True, timeout=120)
+    if proc.returncode != 0:
+        return {"error": f"handoff probe exited {proc.returncode}: {proc.stderr[-500:]}"}
+    out = json.loads(proc.stdout.strip().splitlines()[-1])
+    out["program"] = "littlebit_amd/csrc/handoff_probe.hip"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -587,13 +604,21 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
     ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy",
-                                       "lm_head", "small"], default=None,
+                                       "lm_head", "small", "handoff"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build uses no collectives); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+
+    # the handoff probe is its own program: it runs as a child process before
+    # this process touches the GPU (a process that has initialised the GPU
+    # starts no other program)
+    handoff = None if args.only not in (None, "handoff") else stage_handoff()
+    if args.only == "handoff":
+        print(json.dumps(handoff))
+        return
 
     import torch
     import littlebit_amd._lib as L
@@ -610,6 +635,7 @@ def main():
     if args.only == "lm_head":
         print(json.dumps(lm_head_bench(dev, stream, args.steps, args.warmup)))
         return
+
     if args.only == "small":
         print(json.dumps(small_configs_bench(gen, dev, stream, steps=args.steps, warmup=args.warmup)))
         return
@@ -725,7 +751,8 @@ def main():
                      "launch_floor_ms_per_step": round(floor_us * len(LAYER_CALLS) * args.layers / 1000.0, 4),
                      "launch_floor_note": "smallest decode-path call (K = N = 256, rank 8, M = 1): the latent + "
                                           "expand launches with almost no work, in a graph of 32 calls; a draft "
-                                          f"step is {len(LAYER_CALLS) * args.layers} such calls"},
+                                          f"step is {len(LAYER_CALLS) * args.layers} such calls",
+                     "stage_handoff": handoff},
         "configs_0_1": small,
         "verify_linears": verify_lin,
         "prefill": prefill,

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 7
+#define LBK_ABI_VERSION 8
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -62,6 +62,10 @@ typedef struct lbk_branch {
   const float* mid;      /* [rank]  latent scale l = v1 * u2                */
   const float* u1;       /* [N]     row scale h                             */
   int64_t rank;          /* R >= 1                                          */
+  const int32_t* v_sign_tiled; /* NULL, or v_sign tiled by lbk_tile_v_signs
+                          (16-byte aligned): the decode path (M <= 64)
+                          then reads V from it (whole 128-byte lines per
+                          load); v_sign still serves the GEMM path         */
 } lbk_branch;
 
 /* One projection of a group call: its branches (1 or 2), out_features N,
@@ -268,6 +272,20 @@ int lbk_unpack_signs(const int32_t* packed, int64_t rows, int64_t cols,
  * (quantization/utils/binary_packer.py:5-51) for inputs in {-1, +1}. */
 int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols,
                    int32_t* out, void* stream);
+
+/* Words of V's tiled copy for lbk_branch.v_sign_tiled:
+ * ceil(rank/16) * ceil(ceil(K/32)/4) * 64 (0 for rank or K < 1).  No
+ * counterpart in the reference (a GPU load layout). */
+int64_t lbk_tiled_v_words(int64_t rank, int64_t K);
+
+/* Tile V's sign words [rank, ceil(K/32)] into out (lbk_tiled_v_words
+ * int32, 16-byte aligned): [ceil(rank/16)][ceil(KW/4)][16 rows][4 words],
+ * word w of row r at ((r/16 * ceil(KW/4) + w/4) * 16 + r%16) * 4 + w%4,
+ * zero past rank and past KW = ceil(K/32).  Done once at load time, like the
+ * reference's repack of its sign words for its own kernel
+ * (cpu_draft_model.py:247-250). */
+int lbk_tile_v_signs(const int32_t* v_sign, int64_t rank, int64_t K,
+                     int32_t* out, void* stream);
 
 /* Sign words [rows, words_per_row] -> the 2-bit layout of the reference's CPU
  * runtime, out [rows, ceil(n_cols/4)] uint8, byte for byte what

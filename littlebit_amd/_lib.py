@@ -44,6 +44,7 @@ class LbkBranch(ctypes.Structure):
         ("mid", ctypes.c_void_p),
         ("u1", ctypes.c_void_p),
         ("rank", ctypes.c_int64),
+        ("v_sign_tiled", ctypes.c_void_p),
     ]
 
 
@@ -134,6 +135,8 @@ SIGNATURES = {
     "lbk_unpack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
     "lbk_pack_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
     "lbk_repack_signs_to_i2": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _VP]),
+    "lbk_tiled_v_words": (ctypes.c_int64, [_I64, _I64]),
+    "lbk_tile_v_signs": (ctypes.c_int, [_VP, _I64, _I64, _VP, _VP]),
 }
 
 _lib = None

@@ -185,6 +185,7 @@ static_assert(kTHalf % 4 == 0, "latent halves are read in float4s");
 // Stage-1 operands of one branch ("segment") of a group call.
 struct LatSeg {
   const uint32_t* V;  // [R, KW] sign words
+  const uint32_t* Vt; // the same words tiled (see tile_v_kernel), or null
   const float* g;     // [K]
   const float* l;     // [R]
   int R;
@@ -778,7 +779,32 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   // never stored, and words past the row meet A columns past K, which are
   // zero), so that no wait has to cover a path that skipped a load.
   uint32_t words[WPL];
-  {
+  if (SG.Vt) {
+    // tiled copy [ceil(R/16)][ceil(KW/4)][16 rows][4 words]: the lane's WPL
+    // words are WPL/4 whole 16-byte cells of its row (half a cell at WPL = 2),
+    // and the lanes of a load read whole 128-byte lines.  Rows past R read
+    // row 0 (never stored); cells past the row read cell 0 (they meet A
+    // columns past K, which are zero), as in the untiled path.
+    const int kw4 = (p.KW + 3) >> 2;
+    const int rr = r < R ? r : 0;
+    const uint32_t* __restrict__ cells = SG.Vt + size_t(rr >> 4) * kw4 * 64 + (rr & 15) * 4;
+    if constexpr (WPL == 2) {
+      const int gi = w0 < p.KW ? w0 >> 2 : 0;
+      const uint2 v = *reinterpret_cast<const uint2*>(cells + size_t(gi) * 64 + (w0 & 3));
+      words[0] = v.x;
+      words[1] = v.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < WPL / 4; ++q) {
+        const int gi = (w0 >> 2) + q < kw4 ? (w0 >> 2) + q : 0;
+        const uint4 v = *reinterpret_cast<const uint4*>(cells + size_t(gi) * 64);
+        words[4 * q] = v.x;
+        words[4 * q + 1] = v.y;
+        words[4 * q + 2] = v.z;
+        words[4 * q + 3] = v.w;
+      }
+    }
+  } else {
     const uint32_t* __restrict__ vrow = V + size_t(r < R ? r : 0) * p.KW;
     if (p.wvec) {
       // the lane's WPL words in one or two vector loads: with KW % WPL == 0 a
@@ -2153,6 +2179,27 @@ __global__ __launch_bounds__(kBlock) void pack_kernel(const int8_t* signs, int64
 // masks the columns past n_cols and spreads the 4 bits to bit 7 - 2 g of the
 // 4 bytes.  The word index 4 b + g = c / 32 of a column c < n_cols is below
 // ceil(n_cols / 32) <= wpr (checked by the host).
+// V sign words [R][KW] -> the latent kernel's tiled copy
+// [ceil(R/16)][ceil(KW/4)][16 rows][4 words] (zero past R and past KW): a
+// 16-byte cell holds 4 words of one row, and the 16 rows of a tile lie side by
+// side, so the lanes of one load (16 rows x 4 word groups) read whole 128-byte
+// lines whatever the k-chunk width.  One thread per cell.
+__global__ __launch_bounds__(kBlock) void tile_v_kernel(const uint32_t* __restrict__ v, int64_t R, int64_t KW,
+                                                        u32x4* __restrict__ out) {
+  const int64_t kw4 = (KW + 3) / 4, ncell = (R + 15) / 16 * kw4 * 16;
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < ncell; i += int64_t(gridDim.x) * kBlock) {
+    const int64_t rl = i & 15, gi = (i >> 4) % kw4, t = (i >> 4) / kw4;
+    const int64_t r = 16 * t + rl;
+    u32x4 c = {0u, 0u, 0u, 0u};
+    if (r < R) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (4 * gi + e < KW) c[e] = v[r * KW + 4 * gi + e];
+    }
+    out[i] = c;
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void repack_i2_kernel(const uint32_t* __restrict__ packed, int64_t rows,
                                                            int64_t wpr, int64_t n_cols, int64_t ob, int dword_rows,
                                                            uint8_t* __restrict__ out) {
@@ -2968,6 +3015,8 @@ int validate_group(const ProjDesc* pd, int np, int64_t M, int64_t K) {
                          (long long)B.rank);
       if (!B.v_sign || !B.u_sign || !B.v2 || !B.mid || !B.u1)
         return set_error(LBK_ERR_ARG, "projection %d branch %d: NULL factor or scale pointer", q, b);
+      if (B.v_sign_tiled && (reinterpret_cast<uintptr_t>(B.v_sign_tiled) & 15u))
+        return set_error(LBK_ERR_ARG, "projection %d branch %d: v_sign_tiled must be 16-byte aligned", q, b);
       rsum += B.rank;
     }
   }
@@ -3444,6 +3493,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
       const lbk_branch& B = pd[q].br[b];
       LatSeg& S = p.seg[si];
       S.V = reinterpret_cast<const uint32_t*>(B.v_sign);
+      S.Vt = reinterpret_cast<const uint32_t*>(B.v_sign_tiled);
       S.g = B.v2;
       S.l = B.mid;
       S.R = int(B.rank);
@@ -3460,7 +3510,7 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
       P.tbase[b] = tbase;
       rb += int(ceil_div(B.rank, kRowBlock));
       tbase += int(M) * S.RP;
-      wvec = wvec && (reinterpret_cast<uintptr_t>(B.v_sign) % 16) == 0;
+      wvec = wvec && (B.v_sign_tiled || (reinterpret_cast<uintptr_t>(B.v_sign) % 16) == 0);
       xvec = xvec && (reinterpret_cast<uintptr_t>(B.v2) % 16) == 0;
     }
   }
@@ -3971,7 +4021,7 @@ int lbk_littlebit_linear(const float* input, int64_t M, const float* v2, const i
                          const float* mid, const int32_t* u_sign, int64_t u_cols, const float* u1,
                          int64_t out_features, float* output, void* workspace, size_t workspace_bytes,
                          void* stream) {
-  lbk_branch b;
+  lbk_branch b{};  // no tiled copy: V is read as the reference stores it
   b.v_sign = v_sign;
   b.u_sign = u_sign;
   b.v2 = v2;
@@ -4005,6 +4055,25 @@ int lbk_pack_signs(const int8_t* signs, int64_t rows, int64_t cols, int32_t* out
   hipLaunchKernelGGL(pack_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream), signs,
                      rows, cols, wpr, reinterpret_cast<uint32_t*>(out));
   return check_launch("pack_kernel");
+}
+
+int64_t lbk_tiled_v_words(int64_t rank, int64_t K) {
+  if (rank < 1 || K < 1) return 0;
+  return ceil_div(rank, 16) * ceil_div(ceil_div(K, 32), 4) * 64;
+}
+
+int lbk_tile_v_signs(const int32_t* v_sign, int64_t rank, int64_t K, int32_t* out, void* stream) {
+  g_last_error[0] = '\0';
+  if (rank < 1 || K < 1 || rank > kMaxDim || K > kMaxDim)
+    return set_error(LBK_ERR_ARG, "rank and K must be in [1, %lld], got %lld, %lld", (long long)kMaxDim,
+                     (long long)rank, (long long)K);
+  if (!v_sign || !out) return set_error(LBK_ERR_ARG, "NULL pointer");
+  if (reinterpret_cast<uintptr_t>(out) & 15u) return set_error(LBK_ERR_ARG, "out must be 16-byte aligned");
+  const int64_t ncell = lbk_tiled_v_words(rank, K) / 4;
+  const int64_t blocks = ceil_div(ncell, kBlock) < 65536 ? ceil_div(ncell, kBlock) : 65536;
+  hipLaunchKernelGGL(tile_v_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint32_t*>(v_sign), rank, ceil_div(K, 32), reinterpret_cast<u32x4*>(out));
+  return check_launch("tile_v_kernel");
 }
 
 int lbk_repack_signs_to_i2(const int32_t* packed, int64_t rows, int64_t words_per_row, int64_t n_cols, uint8_t* out,

@@ -221,7 +221,11 @@ class LittleBitProjection:
     """A projection's branches (draft, optional residual) and optional bias,
     prepared once so that each forward is one C call."""
 
-    def __init__(self, branches: Sequence[LittleBitBranch], bias: Optional[torch.Tensor] = None):
+    def __init__(self, branches: Sequence[LittleBitBranch], bias: Optional[torch.Tensor] = None,
+                 tile_v: bool = True):
+        """``tile_v`` (default) keeps a tiled copy of each branch's V words
+        (``lbk_tile_v_signs``) that the decode path (M <= 64) reads with whole
+        128-byte lines per load; the stored words serve every other path."""
         _check(1 <= len(branches) <= 2, "a projection has one or two branches")
         self.branches = list(branches)
         self.in_features = self.branches[0].in_features
@@ -243,6 +247,22 @@ class LittleBitProjection:
             arr[i].mid = b.mid.data_ptr()
             arr[i].u1 = b.u1.data_ptr()
             arr[i].rank = b.rank
+        # the tiled copies, made once here (not under graph capture, where the
+        # projection keeps reading V as stored)
+        self._v_tiled = []
+        if tile_v and not torch.cuda.is_current_stream_capturing():
+            lib = _lib.load()
+            stream = torch.cuda.current_stream(self.device)
+            for i, b in enumerate(self.branches):
+                vt = torch.empty(int(lib.lbk_tiled_v_words(b.rank, self.in_features)), dtype=torch.int32,
+                                 device=self.device)
+                with torch.cuda.device(self.device):
+                    rc = lib.lbk_tile_v_signs(b.v_sign.data_ptr(), b.rank, self.in_features, vt.data_ptr(),
+                                              stream.cuda_stream)
+                _lib.check(rc, "lbk_tile_v_signs")
+                arr[i].v_sign_tiled = vt.data_ptr()
+                self._v_tiled.append(vt)
+            stream.synchronize()  # the copies are complete before any stream uses them
         self._arr = arr
         self._group = None
 

@@ -26,7 +26,7 @@ static int failures = 0;
 static const void* fake(uintptr_t i) { return reinterpret_cast<const void*>(uintptr_t(0x100000) * (i + 1)); }
 
 static lbk_branch branch(int64_t rank, uintptr_t tag) {
-  lbk_branch b;
+  lbk_branch b{};
   b.v_sign = static_cast<const int32_t*>(fake(tag));
   b.u_sign = static_cast<const int32_t*>(fake(tag + 1));
   b.v2 = static_cast<const float*>(fake(tag + 2));

@@ -56,8 +56,9 @@ def test_constants_match_header():
 
 def test_struct_layout():
     import littlebit_amd._lib as L
-    assert ctypes.sizeof(L.LbkBranch) == 6 * 8
+    assert ctypes.sizeof(L.LbkBranch) == 7 * 8
     assert L.LbkBranch.rank.offset == 40
+    assert L.LbkBranch.v_sign_tiled.offset == 48
 
 
 def _branch(rank=8):
