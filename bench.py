@@ -43,6 +43,8 @@ HBM_PEAK_GBS = 8000.0
 # half the bytes moved).  Commands and figures in
 # profiles/littlebit_decode_calls.md; a kind without a measurement reports null.
 MEASURED_TRAFFIC = {"qkv": 1_390_528, "o": 669_856, "gate/up": 2_017_888, "down": 1_485_600}
+# the same for the target's calls at M = 8 (profiles/littlebit_verify_m8_target.md)
+MEASURED_TRAFFIC_M8 = {"qkv": 12_328_960, "o": 6_075_290, "gate/up": 18_509_517, "down": 12_025_242}
 MALL_BYTES = 256 << 20
 
 
@@ -335,20 +337,43 @@ def prefill_bench(gen, dev, stream, steps=20, warmup=3):
             "mfma_frac_executed": round(executed / MFMA_BF16_PEAK_TFLOPS, 4), "us_per_call": per_call}
 
 
-def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5):
+def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5, per_class=True):
     """The ~1.0-BPW target's verify linears: the 224 target projections (draft +
     residual branch each) at M = 8 (a verify of 8 draft tokens), grouped as in the draft step, one HIP graph per
-    pass, weights cold (2 replicas of 0.9 GB rotated)."""
+    pass, weights cold (2 replicas of 0.9 GB rotated).  ``per_class``: each call kind's duration at M = 8 in a
+    graph of 32 calls with distinct weights, and a roofline block for the longest one."""
     import torch
     reps = [DraftStep(gen, dev, layers, M=M, residual=True) for _ in range(2)]
     graphs = [capture(r.run, stream) for r in reps]
     ms = time_graphs(graphs, steps, warmup, stream)
     b = reps[0].bytes
+    del graphs, reps
     gbs = b / (ms * 1e-3) / 1e9
-    return {"workload": f"llama2-7b 1.0-bpw target linears, {layers} layers x 7 projections at M={M} "
-                        "(draft rank 205/298 + residual 1843/2686 per projection), fp32",
-            "ms_per_pass": round(ms, 4), "us_per_layer": round(ms * 1000.0 / layers, 2),
-            "bytes_per_pass": b, "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out = {"workload": f"llama2-7b 1.0-bpw target linears, {layers} layers x 7 projections at M={M} "
+                       "(draft rank 205/298 + residual 1843/2686 per projection), fp32",
+           "ms_per_pass": round(ms, 4), "us_per_layer": round(ms * 1000.0 / layers, 2),
+           "bytes_per_pass": b, "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if not per_class:
+        return out
+    cls = {}
+    for kind, names in LAYER_CALLS:
+        calls = [Call(gen, dev, names, M=M, residual=True) for _ in range(32)]
+        g = capture(lambda: [c.run() for c in calls], stream)
+        us = time_graphs([g], steps, warmup, stream) * 1000.0 / 32
+        cls[kind] = {"projections": "+".join(names), "us_per_call": round(us, 3), "bytes": calls[0].bytes,
+                     "gbs": round(calls[0].bytes / us / 1e3, 2)}
+        del calls, g
+    dom = max(cls, key=lambda c: cls[c]["us_per_call"])
+    d = cls[dom]
+    out["per_class"] = cls
+    out["roofline"] = {"bound": "hbm", "achieved": d["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC_M8.get(dom),
+                       "traffic_source": "not measured in this run: calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE of "
+                                         "the same call kind at M = 8, profiles/littlebit_verify_m8_target.md",
+                       "kernel": f"LittleBitLinear {dom} call at M = {M} ({d['projections']}, draft + residual "
+                                 "branches): latent_mfma_kernel + expand_mfma_kernel",
+                       "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_call"]}
+    return out
 
 
 def decode_bench(dev, draft_len=8, kv_draft=512, kv_target=1024, replays=32, target=True):

@@ -1949,8 +1949,10 @@ __device__ __forceinline__ int64_t sk_start(int b, const SkParams& q) { return i
 // the block whose range holds iteration i: the largest b with sk_start(b) <= i
 __device__ __forceinline__ int sk_block(int64_t i, const SkParams& q) { return int(((i + 1) * q.P - 1) / q.W); }
 
+// Two blocks per CU (the sk_blocks plan assumes them): held to 256 registers
+// per lane (unbounded, the partial-tile code took 256 VGPRs + 64 AGPRs).
 template <bool SPLIT, bool GB>
-__global__ __launch_bounds__(kGThreads) void gemm_latent_sk_kernel(GemmParams p, SkParams q) {
+__global__ __launch_bounds__(kGThreads, 2) void gemm_latent_sk_kernel(GemmParams p, SkParams q) {
   const int tid = int(threadIdx.x);
   const int grp = int(blockIdx.x) % q.G;
   const int b = int(blockIdx.x) / q.G;
@@ -2022,8 +2024,10 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_sk_kernel(GemmParams p,
 }
 
 // Stage 2.  grid = (m-tiles, column tiles of all projections), 256 threads.
+// Held to 256 registers per lane (two waves per SIMD; unbounded, the two
+// accumulator sets took 244 VGPRs + 64 AGPRs, one wave per SIMD).
 template <typename YT, bool SPLIT>
-__global__ __launch_bounds__(kGThreads) void gemm_expand_kernel(GemmParams p) {
+__global__ __launch_bounds__(kGThreads, 2) void gemm_expand_kernel(GemmParams p) {
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
   int pi = 0;
