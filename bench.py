@@ -42,7 +42,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE x 1.0, the factors a 256 MiB device copy reads (FETCH_SIZE counts
 # half the bytes moved).  Commands and figures in
 # profiles/littlebit_decode_calls.md; a kind without a measurement reports null.
-MEASURED_TRAFFIC = {"qkv": 1_390_528, "o": 669_856, "gate/up": 2_017_888, "down": 1_485_600}
+MEASURED_TRAFFIC = {"qkv": 1_418_656, "o": 694_880, "gate/up": 2_002_528, "down": 1_451_904}
 # the same for the target's calls at M = 8 (profiles/littlebit_verify_m8_target.md)
 MEASURED_TRAFFIC_M8 = {"qkv": 12_328_960, "o": 6_075_290, "gate/up": 18_509_517, "down": 12_025_242}
 MALL_BYTES = 256 << 20
