@@ -1143,11 +1143,13 @@ struct SignWords {
 // grid = (sum over projections of ceil(N / (16 * tiles)), ks)
 // LDS: compact A operands of the slice's t chunks, branch 0's then branch 1's
 //
-// Every load the block needs -- the sign words, h, bias and residual, then
-// each thread's first staging chunk (whose address needs the latent-buffer
-// half, read from memory) -- is issued before the first wait on them, at
-// clamped addresses: rows past N are never stored, and sign words past a row
-// meet ranks past R, whose t is zero.
+// Loads are issued in the order they are needed -- the latent-buffer half
+// (the staging addresses depend on it), each thread's first staging tasks,
+// the sign words group by group, then h, bias and residual -- at clamped
+// addresses: rows past N are never stored, and sign words past a row meet
+// ranks past R, whose t is zero.  Vector-memory waits retire loads in issue
+// order, so the staging waits for its own loads only and the MFMA loop for
+// one group of sign words at a time, while the rest are still arriving.
 // ---------------------------------------------------------------------------
 // 8-wave blocks of the 8-row kernel with up to 24 steps per wave are held to
 // 128 VGPRs (four waves per SIMD: two blocks per CU); at 24 steps that
@@ -1209,11 +1211,10 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
   const int ng = (nsteps + 3) / 4;
   const int sb0 = min(4 * (int(blockIdx.y) * ng / ks), nsteps);
   const int sb1 = min(4 * ((int(blockIdx.y) + 1) * ng / ks), nsteps);
+  const uint32_t hq = __builtin_amdgcn_readfirstlane(hq_word) & 1u;
   // block (0, 0, 0) hands the latent buffer on (P = 1 - Q), before any return
-  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0) {
-    const uint32_t q = __hip_atomic_load(p.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.sync, (q & 1u) ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0)
+    __hip_atomic_store(p.sync, hq ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (sb0 >= sb1 || int(blockIdx.x) >= p.ntiles) return;
   // parts of a two-branch sequence start at multiples of 4 (no group spans P0)
   const int len = sb1 - sb0;
@@ -1221,36 +1222,17 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
   const int q0 = sb0 + min(part * per, len);
   const int q1 = min(q0 + per, sb1);
 
-  // (1) sign words of the wave's steps
-  SignWords<S> sw;
-  sw.load(sq, nc, q0, q1, grp);
-  // (2) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
-  const float h0v = P.h[0][nc];
-  const float h1v = P.h[two ? 1 : 0][nc];
-  const float* __restrict__ bsrc = P.bias ? P.bias : P.h[0];
-  const float bnv = bsrc[nc];
-  const bool addres = P.res && ks == 1;  // ks > 1: y already holds the residual
-  const float* __restrict__ rsrc = addres ? P.res : P.h[0];
-  const size_t rstride = addres ? size_t(P.N) : 0;  // no residual: every load reads h[0][0]
-  const int rcol = addres ? nc : 0;
-  float resv[L::MB][4];
-#pragma unroll
-  for (int mb = 0; mb < L::MB; ++mb)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      resv[mb][i] = rsrc[size_t(mrow0 + min(mb * 8 + (grp & 1) * 4 + i, M - 1)) * rstride + rcol];
-
-  // (3) this thread's first staging task (below), issued last: its address
-  // needs the latent-buffer half, read from memory, so the loads that do not
-  // wait for that go first (the staging then waits for every load).  Branch
-  // b's chunks [cb, cb + nchb) of its 16 * steps (16 chunks of 8 ranks per
+  // (1) this thread's first staging tasks (below) go first, the sign words
+  // and epilogue operands after them: vector-memory waits retire loads in
+  // issue order, so the staging waits for its own loads only, and the MFMA
+  // loop waits for each group of sign words as it needs it.  Branch b's
+  // chunks [cb, cb + nchb) of its 16 * steps (16 chunks of 8 ranks per
   // step); with ks = 1 all of them
   const int c0a = 16 * min(sb0, sq.steps[0]);
   const int nch0 = 16 * min(sb1, sq.steps[0]) - c0a;
   const int c1a = two ? 16 * min(max(sb0 - sq.P0, 0), sq.steps[1]) : 0;
   const int nch1 = two ? 16 * min(max(sb1 - sq.P0, 0), sq.steps[1]) - c1a : 0;
   const int nch = nch0 + nch1;
-  const uint32_t hq = __builtin_amdgcn_readfirstlane(hq_word) & 1u;
   const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
   const float* __restrict__ tssq = ta + p.tsize + mrow0;  // the chunk's rows' sums of squares
   u32x4* tb0 = lds_t;
@@ -1339,28 +1321,60 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
 #pragma unroll
     for (int i = 0; i < (MT + 7) / 8; ++i) ssq[i].load(tssq + 8 * i);
   }
-
-  // (4) staging: the first PARTS tasks, then any past the first PARTS * THREADS
+  auto put_first = [&]() {
 #pragma unroll
-  for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
-  if (late) {
-    const float kinv = 1.f / float(p.K), eps = p.eps;
+    for (int m = 0; m < MT; ++m) rsv[m] = 1.f;
+    if (late) {
+      const float kinv = 1.f / float(p.K), eps = p.eps;
 #pragma unroll
-    for (int i = 0; i < (MT + 7) / 8; ++i) {
-      float a[8];
-      ssq[i].get(a);
+      for (int i = 0; i < (MT + 7) / 8; ++i) {
+        float a[8];
+        ssq[i].get(a);
 #pragma unroll
-      for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = inv_rms(a[e], kinv, eps);
+        for (int e = 0; e < 8 && 8 * i + e < MT; ++e) rsv[8 * i + e] = inv_rms(a[e], kinv, eps);
+      }
+    }
+    if (tid < ntask) put_task(tid, v[0]);
+    if constexpr (PARTS == 2) {
+      if (tid + THREADS < ntask) put_task(tid + THREADS, v[1]);
+    }
+  };
+  // A slice with more tasks than PARTS * THREADS stages them all here, before
+  // the sign words are issued: a loop of loads and waits between the sign
+  // loads and the MFMA loop would leave the compiler one full wait for all of
+  // them, which the staged order below exists to avoid
+  const bool tail = ntask > PARTS * THREADS;  // block-uniform
+  if (tail) {
+    put_first();
+    for (int h = tid + PARTS * THREADS; h < ntask; h += THREADS) {
+      load_task(h, v[0]);
+      put_task(h, v[0]);
     }
   }
-  if (tid < ntask) put_task(tid, v[0]);
-  if constexpr (PARTS == 2) {
-    if (tid + THREADS < ntask) put_task(tid + THREADS, v[1]);
-  }
-  for (int h = tid + PARTS * THREADS; h < ntask; h += THREADS) {
-    load_task(h, v[0]);
-    put_task(h, v[0]);
-  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // (2) sign words of the wave's steps
+  SignWords<S> sw;
+  sw.load(sq, nc, q0, q1, grp);
+  // (3) epilogue operands: h, bias, residual rows m = 8 mb + 4 (grp & 1) + i
+  const float h0v = P.h[0][nc];
+  const float h1v = P.h[two ? 1 : 0][nc];
+  const float* __restrict__ bsrc = P.bias ? P.bias : P.h[0];
+  const float bnv = bsrc[nc];
+  const bool addres = P.res && ks == 1;  // ks > 1: y already holds the residual
+  const float* __restrict__ rsrc = addres ? P.res : P.h[0];
+  const size_t rstride = addres ? size_t(P.N) : 0;  // no residual: every load reads h[0][0]
+  const int rcol = addres ? nc : 0;
+  float resv[L::MB][4];
+#pragma unroll
+  for (int mb = 0; mb < L::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      resv[mb][i] = rsrc[size_t(mrow0 + min(mb * 8 + (grp & 1) * 4 + i, M - 1)) * rstride + rcol];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // (4) staging of the first PARTS tasks (when the slice has no more)
+  if (!tail) put_first();
   __syncthreads();
 
   // (5) MFMA over the wave's steps, branch 0 then branch 1: acc holds the
