@@ -317,7 +317,43 @@ def lm_head_bench(dev, stream, steps=100, warmup=10, copies=4):
             "gbs": round(nbytes / us / 1000.0, 1), "launches": 2}
 
 
-def prefill_bench(gen, dev, stream, steps=20, warmup=3):
+def prefill_library_reference(dev, stream, steps=20, warmup=3):
+    """The same layer as plain bf16 GEMMs through the vendor library (torch.matmul -> hipBLASLt), a reference point
+    for the hand-written kernels and not a path of this library: weights already dense bf16 (no sign expansion),
+    stage 1 = x[M, K] @ [V_b]^T over the group's branches concatenated, stage 2 = T_b @ [U_0 | U_1]^T per
+    projection, both weights stored [N, K] (the layout the library ran fastest in at these shapes), 2 copies of the
+    layer rotated, one graph per call kind."""
+    import torch
+    g = torch.Generator().manual_seed(7)
+    rnd = lambda *s: torch.randn(s, generator=g).to(torch.bfloat16).to(dev)  # noqa: E731
+    per_kind, total_ms = {}, 0.0
+    for kind, shapes in PREFILL_LAYER:
+        K = shapes[0][0]
+        rs = sum(sum(ranks) for _, _, ranks in shapes)
+        copies = []
+        for _ in range(2):
+            x = rnd(PREFILL_M, K)
+            w1 = rnd(rs, K)
+            w2 = [(rnd(PREFILL_M, sum(ranks)), rnd(N, sum(ranks))) for _, N, ranks in shapes]
+            copies.append((x, w1, w2))
+
+        def run(c):
+            x, w1, w2 = c
+            torch.matmul(x, w1.t())
+            for t, w in w2:
+                torch.matmul(t, w.t())
+        graphs = [capture(lambda c=c: run(c), stream) for c in copies]
+        ms = time_graphs(graphs, steps, warmup, stream)
+        per_kind[kind] = round(ms * 1000.0, 2)
+        total_ms += ms
+        del graphs, copies
+    flops = sum(proj_flops(PREFILL_M, K, N, ranks) for _, shapes in PREFILL_LAYER for K, N, ranks in shapes)
+    return {"what": "plain bf16 GEMMs of the same shapes through torch.matmul (hipBLASLt) on dense bf16 weights: "
+                    "a reference point, not this library's path", "ms_per_layer": round(total_ms, 4),
+            "tflops": round(flops / (total_ms * 1e-3) / 1e12, 1), "us_per_call": per_kind}
+
+
+def prefill_bench(gen, dev, stream, steps=20, warmup=3, library_reference=True):
     """ms per layer and TFLOP/s of the config-4 linears (2 layers' weights rotated)."""
     layers = [PrefillLayer(gen, dev, PREFILL_M) for _ in range(2)]
     graphs = [capture(l.run, stream) for l in layers]
@@ -328,13 +364,17 @@ def prefill_bench(gen, dev, stream, steps=20, warmup=3):
         per_call[kind] = round(time_graphs(g, steps, warmup, stream) * 1000.0, 2)
     tflops = layers[0].flops / (ms * 1e-3) / 1e12
     executed = layers[0].mfma_flops / (ms * 1e-3) / 1e12
-    return {"workload": "llama3-8b prefill linears, 1 layer (q/k/v, o, gate/up, down; draft + residual branches)",
-            "M": PREFILL_M, "dtype": "bf16", "ms_per_layer": round(ms, 4),
-            "ms_per_forward_32_layers": round(32 * ms, 3), "flops_per_layer": layers[0].flops,
-            "tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
-            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "mfma_flops_executed_per_layer": layers[0].mfma_flops,
-            "mfma_frac_executed": round(executed / MFMA_BF16_PEAK_TFLOPS, 4), "us_per_call": per_call}
+    out = {"workload": "llama3-8b prefill linears, 1 layer (q/k/v, o, gate/up, down; draft + residual branches)",
+           "M": PREFILL_M, "dtype": "bf16", "ms_per_layer": round(ms, 4),
+           "ms_per_forward_32_layers": round(32 * ms, 3), "flops_per_layer": layers[0].flops,
+           "tflops": round(tflops, 1), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+           "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+           "mfma_flops_executed_per_layer": layers[0].mfma_flops,
+           "mfma_frac_executed": round(executed / MFMA_BF16_PEAK_TFLOPS, 4), "us_per_call": per_call}
+    del graphs, layers
+    if library_reference:
+        out["library_reference"] = prefill_library_reference(dev, stream, steps, warmup)
+    return out
 
 
 def verify_linears_bench(gen, dev, stream, layers=32, M=8, steps=50, warmup=5, per_class=True):
