@@ -658,6 +658,22 @@ def stage_handoff(stages: int = 64):
     return out
 
 
+def mfma_issue():
+    """What the GEMM path's mainloop can sustain: 32x32x16 bf16 MFMAs with V
+    independent (or B-operand-rewriting) VALU instructions after each, and
+    with A fragments read from LDS (littlebit_amd/csrc/mfma_issue_probe.hip),
+    at two and three waves per SIMD.  Run as a child process."""
+    import subprocess
+    from littlebit_amd.build import ISSUE_PROBE_PATH
+    if not ISSUE_PROBE_PATH.exists():
+        return {"error": f"{ISSUE_PROBE_PATH} not built (python -m littlebit_amd.build)"}
+    proc = subprocess.run([str(ISSUE_PROBE_PATH)], capture_output=True, text=True, timeout=120)
+    if proc.returncode != 0:
+        return {"error": f"MFMA issue probe exited {proc.returncode}: {proc.stderr[-500:]}"}
+    return {"program": "littlebit_amd/csrc/mfma_issue_probe.hip",
+            "cases": [json.loads(l) for l in proc.stdout.strip().splitlines()]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -669,7 +685,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
     ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy",
-                                       "lm_head", "small", "handoff"], default=None,
+                                       "lm_head", "small", "handoff", "issue"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -683,6 +699,9 @@ def main():
     handoff = None if args.only not in (None, "handoff") else stage_handoff()
     if args.only == "handoff":
         print(json.dumps(handoff))
+        return
+    if args.only == "issue":
+        print(json.dumps(mfma_issue()))
         return
 
     import torch

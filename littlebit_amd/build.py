@@ -19,9 +19,11 @@ SRC = PKG_DIR / "csrc" / "littlebit_amd.hip"
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "liblittlebit_amd.so"
-# a measurement program bench.py runs (`--only handoff`), not part of the library
+# measurement programs bench.py runs (`--only handoff`, `--only issue`), not part of the library
 PROBE_SRC = PKG_DIR / "csrc" / "handoff_probe.hip"
 PROBE_PATH = LIB_DIR / "handoff_probe"
+ISSUE_PROBE_SRC = PKG_DIR / "csrc" / "mfma_issue_probe.hip"
+ISSUE_PROBE_PATH = LIB_DIR / "mfma_issue_probe"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU instructions.
@@ -100,10 +102,14 @@ def build(verbose: bool = False) -> Path:
         probe_tmp = PROBE_PATH.with_suffix(".tmp")
         probe_flags = [f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")]
         probe_proc = _run([hipcc_path(), *probe_flags, str(PROBE_SRC), "-o", str(probe_tmp)], verbose)
+        issue_tmp = ISSUE_PROBE_PATH.with_suffix(".tmp")
+        issue_proc = _run([hipcc_path(), *probe_flags, str(ISSUE_PROBE_SRC), "-o", str(issue_tmp)], verbose)
         err = _finish(lib_proc, "library")
         _finish(asm_proc, "device assembly")
         _finish(probe_proc, "handoff probe")
+        _finish(issue_proc, "MFMA issue probe")
         os.replace(probe_tmp, PROBE_PATH)
+        os.replace(issue_tmp, ISSUE_PROBE_PATH)
         bad = inline_asm_instructions(asm_path.read_text())
     if bad:
         tmp.unlink(missing_ok=True)

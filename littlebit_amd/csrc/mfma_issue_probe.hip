@@ -1,0 +1,159 @@
+// Issue-rate probe for the GEMM path's mainloop on gfx950: how much the VALU
+// work and the LDS reads that feed 32x32x16 bf16 MFMAs cost the MFMA pipe.
+// A standalone program (bench.py --only issue runs it as a child process);
+// it prints one JSON line per case.
+//
+//   valu  V: each wave runs rounds of 8 independent MFMAs (8 accumulator
+//            sets) with V independent VALU instructions after each MFMA;
+//            "dep" variants make those VALU rewrite the next MFMA's B
+//            operand, as the in-register sign expansion does.
+//   lds   U: each 1 KB A fragment read from LDS (ds_read_b128) feeds U MFMAs;
+//            U = 0 reads only (LDS read bandwidth).
+//
+// Grids: 256 threads per block, 512 blocks (two waves per SIMD on 256 CUs)
+// and 768 (three).  Only registers and LDS are used; each thread stores one
+// float at the end, into a buffer of exactly grid x 256 floats.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxBlocks = 768;
+
+template <int V, bool DEP>
+__global__ __launch_bounds__(kThreads, 2) void valu_kernel(float* out, int iters) {
+  f32x16 acc[8];
+  for (int m = 0; m < 8; ++m) acc[m] = f32x16{};
+  const unsigned tid = threadIdx.x;
+  unsigned x0 = tid, x1 = tid * 3u, x2 = tid * 5u, x3 = tid * 7u;
+  unsigned b0 = 0x3F803F80u ^ (x0 << 15), b1 = 0x3F803F80u, b2 = 0x3F803F80u, b3 = 0x3F803F80u ^ (x1 << 31);
+  const u32x4 a = {0x3F803F80u, 0x3F803F80u ^ (x2 << 15), 0x3F803F80u, 0x3F803F80u};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, (u32x4{b0, b1, b2, b3})), acc[m],
+                                                       0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (DEP) {
+          unsigned& d = (v & 3) == 0 ? b0 : (v & 3) == 1 ? b1 : (v & 3) == 2 ? b2 : b3;
+          asm volatile("v_xor_b32 %0, %0, %1" : "+v"(d) : "v"(x0));
+        } else {
+          unsigned& d = (v & 3) == 0 ? x0 : (v & 3) == 1 ? x1 : (v & 3) == 2 ? x2 : x3;
+          asm volatile("v_add_u32 %0, %0, %1" : "+v"(d) : "v"(x3));
+        }
+      }
+    }
+  }
+  float s = 0.f;
+  for (int m = 0; m < 8; ++m)
+    for (int e = 0; e < 16; ++e) s += acc[m][e];
+  out[blockIdx.x * kThreads + tid] = s + float(x0 ^ x1 ^ x2 ^ x3) + float(b0 ^ b3);
+}
+
+template <int U>
+__global__ __launch_bounds__(kThreads, 2) void lds_kernel(float* out, int iters) {
+  __shared__ u32x4 lds[1024];  // 16 KB: 16 fragments of 1 KB
+  const int tid = int(threadIdx.x);
+  for (int i = tid; i < 1024; i += kThreads) lds[i] = u32x4{0x3F803F80u, 0x3F803F80u ^ unsigned(i), 0x3F803F80u, 0u};
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  f32x16 acc[8];
+  for (int m = 0; m < 8; ++m) acc[m] = f32x16{};
+  u32x4 x = {0u, 0u, 0u, 0u};
+  const u32x4 b = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u ^ unsigned(lane << 15), 0x3F803F80u};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int slot = ((it * 8 + m) * 5 + wave * 3) & 15;  // in [0, 16)
+      const u32x4 a = lds[slot * 64 + lane];
+      if constexpr (U == 0) {
+        x ^= a;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          acc[(m * U + u) & 7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc[(m * U + u) & 7], 0, 0, 0);
+      }
+    }
+  }
+  float s = float(x[0] ^ x[1] ^ x[2] ^ x[3]);
+  for (int m = 0; m < 8; ++m)
+    for (int e = 0; e < 16; ++e) s += acc[m][e];
+  out[blockIdx.x * kThreads + tid] = s;
+}
+
+bool ok(hipError_t e, const char* what) {
+  if (e == hipSuccess) return true;
+  fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+  return false;
+}
+
+// mean ms of 5 launches after one warm-up launch
+template <typename K>
+bool time_kernel(K kernel, float* out, int blocks, int iters, hipEvent_t a, hipEvent_t b, float& ms) {
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, 0, out, iters);
+  if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(a), "event")) return false;
+  for (int r = 0; r < 5; ++r) hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, 0, out, iters);
+  if (!ok(hipEventRecord(b), "event") || !ok(hipEventSynchronize(b), "sync")) return false;
+  if (!ok(hipEventElapsedTime(&ms, a, b), "elapsed")) return false;
+  ms /= 5;
+  return true;
+}
+
+constexpr double kMfmaFlops = 32.0 * 32 * 16 * 2;
+
+template <int V, bool DEP>
+bool valu_case(float* out, int blocks, hipEvent_t a, hipEvent_t b) {
+  const int iters = 2000;
+  float ms = 0.f;
+  if (!time_kernel(valu_kernel<V, DEP>, out, blocks, iters, a, b, ms)) return false;
+  const double mfmas = double(blocks) * (kThreads / 64) * iters * 8;
+  printf("{\"case\": \"valu\", \"valu_per_mfma\": %d, \"dependent\": %s, \"blocks\": %d, \"ms\": %.4f, "
+         "\"tflops\": %.1f}\n",
+         V, DEP ? "true" : "false", blocks, ms, mfmas * kMfmaFlops / (ms * 1e-3) / 1e12);
+  fflush(stdout);
+  return true;
+}
+
+template <int U>
+bool lds_case(float* out, int blocks, hipEvent_t a, hipEvent_t b) {
+  const int iters = U == 0 ? 4000 : 4000 / U;
+  float ms = 0.f;
+  if (!time_kernel(lds_kernel<U>, out, blocks, iters, a, b, ms)) return false;
+  const double reads = double(blocks) * (kThreads / 64) * iters * 8;  // wave-wide 1 KB reads
+  printf("{\"case\": \"lds\", \"mfma_per_fragment\": %d, \"blocks\": %d, \"ms\": %.4f, \"lds_bytes_per_clk_per_cu_at_2.4ghz\": "
+         "%.1f, \"tflops\": %.1f}\n",
+         U, blocks, ms, reads * 1024 / (ms * 1e-3) / 2.4e9 / 256, reads * U * kMfmaFlops / (ms * 1e-3) / 1e12);
+  fflush(stdout);
+  return true;
+}
+
+}  // namespace
+
+int main() {
+  float* out = nullptr;
+  if (!ok(hipMalloc(&out, size_t(kMaxBlocks) * kThreads * sizeof(float)), "hipMalloc")) return 1;
+  hipEvent_t a, b;
+  if (!ok(hipEventCreate(&a), "event") || !ok(hipEventCreate(&b), "event")) return 1;
+  bool good = true;
+  for (int blocks : {512, kMaxBlocks}) {
+    good = good && valu_case<0, false>(out, blocks, a, b) && valu_case<2, false>(out, blocks, a, b) &&
+           valu_case<4, false>(out, blocks, a, b) && valu_case<6, false>(out, blocks, a, b) &&
+           valu_case<8, false>(out, blocks, a, b) && valu_case<12, false>(out, blocks, a, b) &&
+           valu_case<4, true>(out, blocks, a, b) && valu_case<8, true>(out, blocks, a, b);
+    good = good && lds_case<0>(out, blocks, a, b) && lds_case<1>(out, blocks, a, b) &&
+           lds_case<2>(out, blocks, a, b) && lds_case<4>(out, blocks, a, b);
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipFree(out);
+  return good ? 0 : 1;
+}
