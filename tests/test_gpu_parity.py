@@ -121,6 +121,17 @@ def test_ragged_shapes(gpu, M, K, N, ranks):
     _check(y, xu, brs, K, N, TOL_F32, what=f"ragged M={M} K={K} N={N} R={ranks}")
 
 
+@pytest.mark.parametrize("M,K,N,ranks", [(1, 256, 300, [8192]), (1, 320, 200, [100, 7000]), (2, 256, 130, [6000]),
+                                         (8, 128, 96, [4600]), (8, 200, 70, [300, 4200])])
+def test_expand_staging_tail(gpu, M, K, N, ranks):
+    """Rank slices with more staging tasks than the expand block has threads: at one row a rank of 7000-8192 is
+    875-1024 chunks of 8 ranks in one slice (one-row calls are not sliced) against at most 768 threads, so the
+    block stages the rest before it issues its sign words; at 2 and 8 rows whichever slices the planner picks."""
+    x, brs = _synthetic(4242 + M + ranks[-1], M, K, N, ranks)
+    y, xu = _run(gpu, x, brs)
+    _check(y, xu, brs, K, N, TOL_F32, what=f"tail M={M} K={K} N={N} ranks={ranks}")
+
+
 def test_bias(gpu):
     K, N = 300, 200
     x, brs = _synthetic(5, 4, K, N, [40, 70])
