@@ -1643,12 +1643,11 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
   }
 }
 
-// acc[i][j] += A[m0 + 64*wm + 32*i + .., :64*nks] . S[:64*nks, c0 + 32*NJ*wn + 32*j + ..]
+// acc[i][j] += A[m0 + gemm_row(wm, i) + .., :64*nks] . S[:64*nks, c0 + gemm_col<NJ>(wn, j) + ..]
 // S[k, c] = sign bit k of row c of W (ldw words per row, zero past it);
 // step ks reads words 2*ks and 2*ks + 1.  The block covers 128 rows of A and
-// 64 * NJ columns: wave tiles of 64 x 64 (NJ = 2) or 64 x 128 (NJ = 4; each
-// A fragment read from LDS then feeds four MFMAs, and each staged A tile
-// serves twice the columns).
+// BN = 128 or 256 columns (wide: each staged A tile serves twice the
+// columns), its 4 waves laid out as below.
 //
 // A tiles (128 rows x 64 k per plane, rows past M repeat row M - 1) go from
 // global memory straight to LDS (global_load_lds_dwordx4) through a ring of
@@ -1660,8 +1659,8 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
 // -- 8 of each row parity, at the same offset mod 256 -- read 16 distinct
 // 16-byte bank groups (with c ^ (r & 7), rows r and r + 8 collided).
 //
-// The sign words of a step (2 per column, 64 * NJ columns) are fetched by
-// the whole block, NJ / 2 words per thread (columns 128 u + tid / 2, word
+// The sign words of a step (2 per column, BN columns) are fetched by the
+// whole block, BN / 128 words per thread (columns 128 u + tid / 2, word
 // tid % 2), and written to one of two LDS buffers ([column][2 words]) from
 // which every lane of the step reads its columns' pair (8 bytes).  A lane fetching
 // its own columns' words instead costs 16 loads per block and step, each
@@ -1671,7 +1670,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
 // +-g[k] instead of +-1: the 64 g values of a step are staged beside its
 // sign words, as bf16, in one of two 128-byte buffers (each wave fetches
 // them, wave 0 writes them), and each 16-k sub-step reads its 8 values.
-// In wide tiles (NJ = 4) with h given (the second branch of stage 2, h0 the
+// In wide tiles (BN = 256) with h given (the second branch of stage 2, h0 the
 // first branch's row scale) it is +-1 where the lane's column c keeps
 // branch 1 (use_branch1(h0[c], h[c])) and 0 elsewhere; both branches run
 // the same instantiation, so they share one stage ring.
@@ -1686,30 +1685,60 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
 // the stage and the register that step ks - 1 used.  Ends with a barrier.
 constexpr int kGStages = 4;
 
-template <bool SPLIT, bool GB = false, int NJ = 2>
+// Wave layout of a GEMM block: kGWM waves along m, kGWN along the columns;
+// a wave holds kGMI x NJ tiles of 32 x 32 (NJ = BN / (32 kGWN)).  The B
+// operand is expanded in registers from the sign words, once per wave for
+// each of its column tiles, and feeds the kGMI MFMAs of that column; each A
+// fragment read from LDS feeds NJ.  Tall wave tiles (kGWM = 1: all 128 rows,
+// 4 x 1 tiles at BN = 128, 4 x 2 at BN = 256) expand each sign once per
+// block, half the VALU per MFMA of 2 x 2 waves, and read each A fragment for
+// NJ MFMAs instead of 2 NJ: measured, MFMAs fed from LDS lose about 1 % at
+// one fragment per MFMA, while VALU beyond about 4 per MFMA stalls the MFMA
+// pipe (bench.py --only issue).
+#ifndef LBK_GEMM_WM
+#define LBK_GEMM_WM 1
+#endif
+constexpr int kGWM = LBK_GEMM_WM;
+constexpr int kGWN = 4 / kGWM;
+constexpr int kGMI = kGB / (32 * kGWM);
+static_assert(kGWM == 1 || kGWM == 2, "wave layouts 1 x 4 and 2 x 2");
+template <int BN>
+constexpr int gemm_nj() {
+  return BN / (32 * kGWN);
+}
+__device__ __forceinline__ int gemm_row(int wm, int i) { return 32 * kGMI * wm + 32 * i; }
+template <int NJ>
+__device__ __forceinline__ int gemm_col(int wn, int j) {
+  return 32 * NJ * wn + 32 * j;
+}
+__device__ __forceinline__ int gemm_wm(int wave) { return kGWM == 1 ? 0 : wave >> 1; }
+__device__ __forceinline__ int gemm_wn(int wave) { return kGWM == 1 ? wave : wave & 1; }
+
+template <bool SPLIT, bool GB = false, int BN = 128>
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t plane, int64_t lda, int M,
                                               int m0, const uint32_t* __restrict__ W, int ldw, int ncols, int c0,
-                                              int nks, f32x16 (&acc)[2][NJ], int tid,
+                                              int nks, f32x16 (&acc)[kGMI][gemm_nj<BN>()], int tid,
                                               const float* __restrict__ g = nullptr, int kbase = 0,
                                               const float* __restrict__ h = nullptr,
                                               const float* __restrict__ h0 = nullptr) {
-  static_assert(NJ == 2 || NJ == 4, "wave tiles of 64 x 64 or 64 x 128");
-  static_assert(NJ == 2 || !GB, "wide tiles carry no g in the B operand");
+  static_assert(BN == 128 || BN == 256, "blocks of 128 or 256 columns");
+  static_assert(BN == 128 || !GB, "wide tiles carry no g in the B operand");
+  constexpr int NJ = gemm_nj<BN>();
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
   typedef __attribute__((address_space(1))) void* glb_ptr_t;
   constexpr int NT = SPLIT ? 2 : 1;
-  constexpr int NW = NJ / 2;                // sign words per thread and step
+  constexpr int NW = BN / 128;              // sign words per thread and step
   constexpr int TILE = kGB * kGK;           // elements per plane per stage
   constexpr int LOADS_PER_FILL = 4 * NT + NW + (GB ? 1 : 0);  // global_load_lds, sign words, g; per wave
   __shared__ __attribute__((aligned(16))) uint16_t st0[NT * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t st1[NT * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t st2[NT * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t st3[NT * TILE];
-  __shared__ __attribute__((aligned(16))) uint32_t sw[2][2 * 64 * NJ];
+  __shared__ __attribute__((aligned(16))) uint32_t sw[2][2 * BN];
   __shared__ __attribute__((aligned(16))) uint16_t gb[2][kGK];
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = gemm_wm(wave), wn = gemm_wn(wave);
   const int lr = lane & 31, lh = lane >> 5;
   // Steps are numbered from kbase (the first k-step of the range, 64 k
   // each); step st of the range is k-step kbase + st of the matrices.
@@ -1748,10 +1777,10 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   // h is given and the column drops branch 1 (columns past ncols have zero
   // sign words)
   uint32_t hv[NJ];
-  if constexpr (NJ == 4) {
+  if constexpr (BN == 256) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const int n = min(c0 + 32 * NJ * wn + 32 * j + lr, ncols - 1);
+      const int n = min(c0 + gemm_col<NJ>(wn, j) + lr, ncols - 1);
       hv[j] = !h || use_branch1(h0[n], h[n]) ? 0x3F803F80u : 0u;
     }
   }
@@ -1793,7 +1822,7 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
     uint32_t w[NJ][2];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const uint2 pr = *reinterpret_cast<const uint2*>(&sw[ks & 1][2 * (32 * NJ * wn + 32 * j + lr)]);
+      const uint2 pr = *reinterpret_cast<const uint2*>(&sw[ks & 1][2 * (gemm_col<NJ>(wn, j) + lr)]);
       w[j][0] = pr.x;
       w[j][1] = pr.y;
     }
@@ -1803,12 +1832,12 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         b[j] = GB   ? signs_times_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask, gk[s])
-               : NJ == 4 ? signs_times_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask,
+               : BN == 256 ? signs_times_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask,
                                                u32x4{hv[j], hv[j], hv[j], hv[j]})
                     : signs_to_bf16x8(w[j][s >> 1] >> (8 * lh), 2 * (s & 1), kmask, kone);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = 64 * wm + 32 * i + lr;
+      for (int i = 0; i < kGMI; ++i) {
+        const int r = gemm_row(wm, i) + lr;
         const int off = r * kGK + (((2 * s + lh) ^ ((r ^ (r >> 3)) & 7)) << 3);
         const bf16x8 ah = *reinterpret_cast<const bf16x8*>(a + off);
 #pragma unroll
@@ -1873,22 +1902,24 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
 }
 
 // Stage 1 epilogue: T rows of the tile (m0, c0) of segment G, l-scaled.
+constexpr int kGNJ = gemm_nj<kGB>();  // column tiles per wave of a 128-column block
+
 template <bool SPLIT>
 __device__ __forceinline__ void latent_store(const GemmParams& p, const GemmSeg& G, int m0, int c0,
-                                             const f32x16 (&acc)[2][2], int tid) {
+                                             const f32x16 (&acc)[kGMI][kGNJ], int tid) {
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = gemm_wm(wave), wn = gemm_wn(wave);
   const int lr = lane & 31, lh = lane >> 5;
   uint16_t* __restrict__ T = p.t + G.tbase;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = c0 + 64 * wn + 32 * j + lr;  // < RP; rows R <= r < RP are written as zeros
+  for (int j = 0; j < kGNJ; ++j) {
+    const int r = c0 + gemm_col<kGNJ>(wn, j) + lr;  // < RP; rows R <= r < RP are written as zeros
     const float lv = r < G.R ? G.l[r] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kGMI; ++i)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+        const int m = m0 + gemm_row(wm, i) + 8 * (q >> 2) + 4 * lh + (q & 3);
         if (m < p.M) {
           const int64_t o = int64_t(m) * G.RP + r;
           const float v = lv * acc[i][j][q];
@@ -1922,11 +1953,11 @@ __global__ __launch_bounds__(kGThreads) void gemm_latent_kernel(GemmParams p) {
   const GemmSeg& G = p.seg[latent_segment(p, nt)];
   const int m0 = int(blockIdx.x) * kGB;
   const int c0 = (nt - G.nt0) * kGB;
-  f32x16 acc[2][2];
+  f32x16 acc[kGMI][kGNJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < kGNJ; ++j) acc[i][j] = f32x16{};
   gemm_mainloop<SPLIT, GB>(p.a + G.abase, p.a_plane, p.Kp, p.M, m0, G.V, p.KW, G.R, c0, p.Kp / kGK, acc, tid, G.g);
   latent_store<SPLIT>(p, G, m0, c0, acc, tid);
 }
@@ -1983,11 +2014,11 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_latent_sk_kernel(GemmParams
     const GemmSeg& G = p.seg[latent_segment(p, nt)];
     const int m0 = ((t / q.NT) * q.G + grp) * kGB;
     const int c0 = (nt - G.nt0) * kGB;
-    f32x16 acc[2][2];
+    f32x16 acc[kGMI][kGNJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+      for (int j = 0; j < kGNJ; ++j) acc[i][j] = f32x16{};
     gemm_mainloop<SPLIT, GB>(p.a + G.abase, p.a_plane, p.Kp, p.M, m0, G.V, p.KW, G.R, c0, n, acc, tid, G.g, k0);
     bool store = true;
     if (n < q.nks) {
@@ -1995,12 +2026,12 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_latent_sk_kernel(GemmParams
       const int bf = sk_block(ts, q);
       float* __restrict__ mine = q.part + (size_t(gb0 + b) * 2 + (k0 > 0 ? 0 : 1)) * (64 * kGThreads);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kGNJ; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            __hip_atomic_store(mine + ((i * 2 + j) * 16 + e) * kGThreads + tid, acc[i][j][e], __ATOMIC_RELAXED,
+            __hip_atomic_store(mine + ((i * kGNJ + j) * 16 + e) * kGThreads + tid, acc[i][j][e], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
       __syncthreads();
@@ -2016,19 +2047,19 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_latent_sk_kernel(GemmParams
         // block completes the tile: the sum is the same on every run
         const int bl = sk_block(ts + q.nks - 1, q);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+          for (int j = 0; j < kGNJ; ++j) acc[i][j] = f32x16{};
         for (int o = bf; o <= bl; ++o) {
           float* __restrict__ part =
               q.part + (size_t(gb0 + o) * 2 + (sk_start(o, q) > ts ? 0 : 1)) * (64 * kGThreads);
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < kGNJ; ++j)
 #pragma unroll
               for (int e = 0; e < 16; ++e)
-                acc[i][j][e] += __hip_atomic_load(part + ((i * 2 + j) * 16 + e) * kGThreads + tid, __ATOMIC_RELAXED,
+                acc[i][j][e] += __hip_atomic_load(part + ((i * kGNJ + j) * 16 + e) * kGThreads + tid, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
         }
         if (tid == 0) __hip_atomic_store(q.cnt + gb0 + bf, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2053,11 +2084,11 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_kernel(GemmParams p)
   const GemmProj& P = p.proj[pi];
   const int m0 = int(blockIdx.x) * kGB;
   const int c0 = (nt - P.nt0) * kGB;
-  f32x16 acc0[2][2], acc1[2][2];
+  f32x16 acc0[kGMI][kGNJ], acc1[kGMI][kGNJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kGMI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc0[i][j] = acc1[i][j] = f32x16{};
+    for (int j = 0; j < kGNJ; ++j) acc0[i][j] = acc1[i][j] = f32x16{};
   // T rows are zero from R to RP >= 64 * ceil(RW / 2), so whole 64-k steps are safe
   gemm_mainloop<SPLIT>(p.t + P.tbase[0], p.t_plane, P.RP[0], p.M, m0, P.U[0], P.RW[0], P.N, c0, (P.RW[0] + 1) / 2,
                        acc0, tid);
@@ -2066,22 +2097,22 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_kernel(GemmParams p)
                          (P.RW[1] + 1) / 2, acc1, tid);
 
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = gemm_wm(wave), wn = gemm_wn(wave);
   const int lr = lane & 31, lh = lane >> 5;
   YT* __restrict__ y = static_cast<YT*>(P.y);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = c0 + 64 * wn + 32 * j + lr;
+  for (int j = 0; j < kGNJ; ++j) {
+    const int n = c0 + gemm_col<kGNJ>(wn, j) + lr;
     if (n >= P.N) continue;
     const float h0 = P.h[0][n];
     const float h1 = P.nb > 1 ? P.h[1][n] : 0.f;
     const float bn = P.bias ? P.bias[n] : 0.f;
     const float* res = P.res;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kGMI; ++i)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+        const int m = m0 + gemm_row(wm, i) + 8 * (q >> 2) + 4 * lh + (q & 3);
         if (m < p.M) {
           const size_t o = size_t(m) * P.N + n;
           store_out(y, o, h0 * acc0[i][j][q] + h1 * acc1[i][j][q] + bn + (res ? res[o] : 0.f));
@@ -2091,7 +2122,7 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_kernel(GemmParams p)
 }
 
 // Stage 2 on bf16 activations in wide tiles.  grid = (m-tiles, 256-column
-// tiles of all projections), 256 threads; wave tiles of 64 x 128, one set of
+// tiles of all projections), 256 threads (4 waves as in gemm_mainloop), one set of
 // accumulators for both branches (two sets would not fit two blocks per CU):
 // acc = S0 after branch 0 (S_b = sum_r sU_b[n, r] * T_b[m, r]), each column's
 // acc times h0 / h1 in fp32, then branch 1 added: y = h1 * acc = h0 * S0 + h1
@@ -2101,7 +2132,7 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_kernel(GemmParams p)
 // 2^-40 of h0 times |S1 / S0|.
 template <typename YT>
 __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmParams p) {
-  constexpr int NJ = 4, BN = 64 * NJ;
+  constexpr int BN = 2 * kGB, NJ = gemm_nj<BN>();
   const int tid = int(threadIdx.x);
   const int nt = int(blockIdx.y);
   int pi = 0;
@@ -2112,20 +2143,20 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmPara
   const int m0 = int(blockIdx.x) * kGB;
   const int c0 = (nt - P.nt0) * BN;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = gemm_wm(wave), wn = gemm_wn(wave);
   const int lr = lane & 31, lh = lane >> 5;
-  f32x16 acc[2][NJ];
+  f32x16 acc[kGMI][NJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kGMI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = f32x16{};
   // T rows are zero from R to RP >= 64 * ceil(RW / 2), so whole 64-k steps are safe
-  gemm_mainloop<false, false, NJ>(p.t + P.tbase[0], p.t_plane, P.RP[0], p.M, m0, P.U[0], P.RW[0], P.N, c0,
+  gemm_mainloop<false, false, BN>(p.t + P.tbase[0], p.t_plane, P.RP[0], p.M, m0, P.U[0], P.RW[0], P.N, c0,
                                   (P.RW[0] + 1) / 2, acc, tid, nullptr, 0, nullptr);
   float f[NJ];  // the factor y takes of acc, per subtile column
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int n = min(c0 + 32 * NJ * wn + 32 * j + lr, P.N - 1);
+    const int n = min(c0 + gemm_col<NJ>(wn, j) + lr, P.N - 1);
     const float h0 = P.h[0][n];
     const float h1 = P.nb > 1 ? P.h[1][n] : 0.f;
     const bool use1 = P.nb > 1 && use_branch1(h0, h1);
@@ -2133,25 +2164,25 @@ __global__ __launch_bounds__(kGThreads, 2) void gemm_expand_wide_kernel(GemmPara
     if (use1) {
       const float r = h0 / h1;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) acc[i][j] *= r;
+      for (int i = 0; i < kGMI; ++i) acc[i][j] *= r;
     }
   }
   if (P.nb > 1)
-    gemm_mainloop<false, false, NJ>(p.t + P.tbase[1], p.t_plane, P.RP[1], p.M, m0, P.U[1], P.RW[1], P.N, c0,
+    gemm_mainloop<false, false, BN>(p.t + P.tbase[1], p.t_plane, P.RP[1], p.M, m0, P.U[1], P.RW[1], P.N, c0,
                                     (P.RW[1] + 1) / 2, acc, tid, nullptr, 0, P.h[1], P.h[0]);
 
   YT* __restrict__ y = static_cast<YT*>(P.y);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int n = c0 + 32 * NJ * wn + 32 * j + lr;
+    const int n = c0 + gemm_col<NJ>(wn, j) + lr;
     if (n >= P.N) continue;
     const float bn = P.bias ? P.bias[n] : 0.f;
     const float* res = P.res;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kGMI; ++i)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+        const int m = m0 + gemm_row(wm, i) + 8 * (q >> 2) + 4 * lh + (q & 3);
         if (m < p.M) {
           const size_t o = size_t(m) * P.N + n;
           store_out(y, o, f[j] * acc[i][j][q] + bn + (res ? res[o] : 0.f));
