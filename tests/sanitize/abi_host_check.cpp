@@ -109,6 +109,19 @@ int main() {
          "NULL workspace");
   EXPECT(lbk_group_forward(&p1, 1, 8, 4096, xf, LBK_F32, LBK_F32, ws, wsz - 1, nullptr) == LBK_ERR_WORKSPACE,
          "small workspace");
+  // the mode is read once per call, when the call is planned: a workspace
+  // sized with deterministic mode off is refused, before any launch, by a
+  // call made after the mode was turned on (side-by-side row chunks off,
+  // sequential chunks with k-chunk partials on)
+  for (int64_t M : {int64_t(1), int64_t(8), int64_t(33), int64_t(48)}) {
+    const size_t off = lbk_group_workspace_bytes(&p1, 1, M, 4096);
+    lbk_set_deterministic(1);
+    const size_t on = lbk_group_workspace_bytes(&p1, 1, M, 4096);
+    EXPECT(on > off && off > 0, "deterministic workspace M=%lld: %zu vs %zu", (long long)M, on, off);
+    EXPECT(lbk_group_forward(&p1, 1, M, 4096, xf, LBK_F32, LBK_F32, ws, off, nullptr) == LBK_ERR_WORKSPACE,
+           "mode turned on after the query, M=%lld", (long long)M);
+    lbk_set_deterministic(0);
+  }
   {
     lbk_projection p = p1;
     p.y = nullptr;
