@@ -9,10 +9,14 @@
 //            operand, as the in-register sign expansion does.
 //   lds   U: each 1 KB A fragment read from LDS (ds_read_b128) feeds U MFMAs;
 //            U = 0 reads only (LDS read bandwidth).
+//   ring:    the GEMM mainloop's skeleton without the sign expansion
+//            (ring_kernel below), with and without the A-tile loads.
 //
 // Grids: 256 threads per block, 512 blocks (two waves per SIMD on 256 CUs)
-// and 768 (three).  Only registers and LDS are used; each thread stores one
-// float at the end, into a buffer of exactly grid x 256 floats.
+// and 768 (three; not for ring, whose 64 KB of LDS fit two blocks per CU).
+// The valu and lds cases use only registers and LDS; ring reads a 4 MiB
+// buffer, every address inside it.  Each thread stores one float at the end,
+// into a buffer of exactly grid x 256 floats.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -90,6 +94,102 @@ __global__ __launch_bounds__(kThreads, 2) void lds_kernel(float* out, int iters)
   out[blockIdx.x * kThreads + tid] = s;
 }
 
+// The GEMM mainloop's skeleton without the sign expansion: 4 waves, a 4-stage
+// LDS ring of 128 x 64 bf16 A tiles (16 KB each), one barrier per k-step, and
+// per wave and step 16 MFMAs (4 row tiles x 4 sub-steps of 16 k) on A
+// fragments read from the step's stage and a fixed B.  The A tiles come from
+// a 4 MiB buffer (block b, step s: tile (7 b + s) mod 256), which the L2 and
+// the Infinity Cache hold:
+//   MODE 0: no A loads (the ring holds what the first steps left);
+//   MODE 1: global_load_lds_dwordx4 straight into the stage 3 steps ahead,
+//           waited for with vmcnt before the step's barrier (as the library);
+//   MODE 2: global_load_dwordx4 into registers 2 steps ahead, ds_write_b128
+//           into the stage one step ahead.
+constexpr int kTileElems = 128 * 64;
+// s_waitcnt immediates (gfx9 encoding): vmcnt(vm) with lgkmcnt(0), and
+// lgkmcnt(0) alone
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4); }
+constexpr int kWaitLgkm0 = waitcnt_vm_lgkm0(63);
+constexpr int kSrcTiles = 256;  // 4 MiB of bf16
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void ring_kernel(const uint16_t* __restrict__ src, float* out, int steps) {
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  typedef __attribute__((address_space(1))) void* glb_ptr_t;
+  __shared__ __attribute__((aligned(16))) uint16_t st[4][kTileElems];
+  const int tid = int(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  f32x16 acc[4];
+  for (int i = 0; i < 4; ++i) acc[i] = f32x16{};
+  const u32x4 b = {0x3F803F80u, 0x3F803F80u ^ unsigned(lane << 15), 0x3F803F80u, 0x3F803F80u};
+  for (int i = tid; i < 4 * kTileElems / 8; i += kThreads)
+    reinterpret_cast<u32x4*>(&st[0][0])[i] = u32x4{0x3F803F80u, unsigned(i), 0x3F803F80u, 0u};
+  __syncthreads();
+  // element offset of this lane's 16 bytes in slot j of a tile, and of tile s
+  auto lane_elem = [&](int j) { return (wave * 4 + j) * 512 + lane * 8; };
+  auto tile_of = [&](int s) { return size_t((7 * int(blockIdx.x) + s) % kSrcTiles) * kTileElems; };
+  auto dma = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(src + tile_of(s) + lane_elem(j)),
+                                       (lds_ptr_t)(&st[s & 3][(wave * 4 + j) * 512]), 16, 0, 0);
+  };
+  u32x4 reg[2][4];
+  auto gload = [&](int s, u32x4 (&r)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const u32x4*>(src + tile_of(s) + lane_elem(j));
+  };
+  auto gput = [&](int s, const u32x4 (&r)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(&st[s & 3][lane_elem(j)]) = r[j];
+  };
+  if constexpr (MODE == 1) {
+    dma(0);
+    dma(1);
+    dma(2);
+  }
+  if constexpr (MODE == 2) {
+    gload(0, reg[0]);
+    gload(1, reg[1]);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0): both register sets landed
+    gput(0, reg[0]);
+    gload(2, reg[0]);
+  }
+  // one k-step; step ks writes the registers of step ks + 1 (loaded two steps
+  // before) into their stage and loads step ks + 3 into the same set
+  auto step = [&](int ks, u32x4 (&r)[4]) {
+    if constexpr (MODE == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(8));  // fills ks + 1, ks + 2 in flight
+    if constexpr (MODE == 2) {
+      gput(ks + 1, r);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if constexpr (MODE == 1) dma(ks + 3);
+    if constexpr (MODE == 2) gload(ks + 3, r);
+    const uint16_t* a = st[ks & 3];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 32 * i + lr;  // chunk swizzle of the library's A tiles (no bank conflicts)
+        const u32x4 af = *reinterpret_cast<const u32x4*>(a + r * 64 + (((2 * s + lh) ^ ((r ^ (r >> 3)) & 7)) << 3));
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
+                                                         __builtin_bit_cast(bf16x8, b), acc[i], 0, 0, 0);
+      }
+  };
+  for (int ks = 0; ks + 2 <= steps; ks += 2) {  // steps is even
+    step(ks, reg[1]);
+    step(ks + 1, reg[0]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  float sum = 0.f;
+  for (int i = 0; i < 4; ++i)
+    for (int e = 0; e < 16; ++e) sum += acc[i][e];
+  out[blockIdx.x * kThreads + tid] = sum;
+}
+
 bool ok(hipError_t e, const char* what) {
   if (e == hipSuccess) return true;
   fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
@@ -136,6 +236,24 @@ bool lds_case(float* out, int blocks, hipEvent_t a, hipEvent_t b) {
   return true;
 }
 
+template <int MODE>
+bool ring_case(const uint16_t* src, float* out, int blocks, hipEvent_t a, hipEvent_t b) {
+  const int steps = 2000;
+  hipLaunchKernelGGL((ring_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
+  if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(a), "event")) return false;
+  for (int r = 0; r < 5; ++r) hipLaunchKernelGGL((ring_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
+  float ms = 0.f;
+  if (!ok(hipEventRecord(b), "event") || !ok(hipEventSynchronize(b), "sync") || !ok(hipEventElapsedTime(&ms, a, b), "t"))
+    return false;
+  ms /= 5;
+  const double mfmas = double(blocks) * (kThreads / 64) * steps * 16;
+  printf("{\"case\": \"ring\", \"a_tiles\": \"%s\", \"blocks\": %d, \"ms\": %.4f, \"tflops\": %.1f}\n",
+         MODE == 0 ? "none" : MODE == 1 ? "global_load_lds" : "global_load + ds_write", blocks, ms,
+         mfmas * kMfmaFlops / (ms * 1e-3) / 1e12);
+  fflush(stdout);
+  return true;
+}
+
 }  // namespace
 
 int main() {
@@ -144,6 +262,12 @@ int main() {
   hipEvent_t a, b;
   if (!ok(hipEventCreate(&a), "event") || !ok(hipEventCreate(&b), "event")) return 1;
   bool good = true;
+  uint16_t* src = nullptr;
+  if (!ok(hipMalloc(&src, size_t(kSrcTiles) * kTileElems * sizeof(uint16_t)), "hipMalloc") ||
+      !ok(hipMemset(src, 0x3F, size_t(kSrcTiles) * kTileElems * sizeof(uint16_t)), "hipMemset"))
+    return 1;
+  good = good && ring_case<0>(src, out, 512, a, b) && ring_case<1>(src, out, 512, a, b) &&
+         ring_case<2>(src, out, 512, a, b);
   for (int blocks : {512, kMaxBlocks}) {
     good = good && valu_case<0, false>(out, blocks, a, b) && valu_case<2, false>(out, blocks, a, b) &&
            valu_case<4, false>(out, blocks, a, b) && valu_case<6, false>(out, blocks, a, b) &&
@@ -155,5 +279,6 @@ int main() {
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   (void)hipFree(out);
+  (void)hipFree(src);
   return good ? 0 : 1;
 }
