@@ -662,7 +662,8 @@ def mfma_issue():
     """What the GEMM path's mainloop can sustain: 32x32x16 bf16 MFMAs with V
     independent (or B-operand-rewriting) VALU instructions after each, and
     with A fragments read from LDS (littlebit_amd/csrc/mfma_issue_probe.hip),
-    at two and three waves per SIMD.  Run as a child process."""
+    at two and three waves per SIMD, and the mainloop's skeleton with and
+    without its A-tile loads.  Run as a child process."""
     import subprocess
     from littlebit_amd.build import ISSUE_PROBE_PATH
     if not ISSUE_PROBE_PATH.exists():
