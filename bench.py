@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0
 # profiles/littlebit_decode_calls.md; a kind without a measurement reports null.
 MEASURED_TRAFFIC = {"qkv": 1_418_656, "o": 694_880, "gate/up": 2_002_528, "down": 1_451_904}
 # the same for the target's calls at M = 8 (profiles/littlebit_verify_m8_target.md)
-MEASURED_TRAFFIC_M8 = {"qkv": 12_328_960, "o": 6_075_290, "gate/up": 18_509_517, "down": 12_025_242}
+MEASURED_TRAFFIC_M8 = {"qkv": 11_636_122, "o": 5_105_971, "gate/up": 17_666_765, "down": 9_626_419}
 MALL_BYTES = 256 << 20
 
 

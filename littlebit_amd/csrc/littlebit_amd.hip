@@ -219,6 +219,7 @@ struct MfmaParams {
                 // [c * crows, min(M, (c + 1) * crows)); crows = M with one chunk
   int tsize;    // M * sum(RP) floats
   int nkc;      // k-chunks
+  int kc_major; // latent blocks in k-chunk-major order (every segment reads V's tiled copy)
   int splits;   // expand_mfma_kernel: waves sharing the rank steps of a 16-row tile
   int ntiles;   // expand_mfma_kernel: row tiles of all projections (grid.x may be padded)
   int ks;       // expand_mfma_kernel: rank slices per projection (grid.y); with ks > 1
@@ -744,9 +745,15 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   constexpr int KC = 128 * WPL;
   constexpr int NCH = KC / 8;  // 8-column chunks per k-chunk
 
+  // Logical block lb: each XCD runs a contiguous range of them.  Row-block
+  // major (the k-chunks of a row-block on one XCD) when V is read as stored:
+  // neighbouring k-chunks then share 128-byte lines of the sign rows.  With
+  // V's tiled copy no line spans two k-chunks, and k-chunk major order has
+  // each XCD fetch its own share of the input rows instead of all of them.
   const int lb = xcd_contiguous_block(int(blockIdx.x), int(gridDim.x));
-  const int rbk = lb / p.nkc;
-  const int kc = lb - rbk * p.nkc;
+  const int nrbt = int(gridDim.x) / p.nkc;  // row-blocks of all segments
+  const int kc = p.kc_major ? lb / nrbt : lb % p.nkc;
+  const int rbk = p.kc_major ? lb - kc * nrbt : lb / p.nkc;
   // segment of this row-block: a wave-uniform index, so the descriptor is
   // read with scalar loads from the kernel arguments
   int si = 0;
@@ -3571,6 +3578,8 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.nseg = si;
   p.tsize = tbase;
   p.nkc = pl.nkc;
+  p.kc_major = 1;
+  for (int i = 0; i < si; ++i) p.kc_major = p.kc_major && p.seg[i].Vt ? 1 : 0;
   // rows past the plan's tile (a call planned in row chunks): the chunks run
   // side by side in the same two launches
   p.crows = pl.chunk > 0 ? pl.chunk : int(M);
