@@ -42,7 +42,7 @@ HBM_PEAK_GBS = 8000.0
 # WRITE_SIZE x 1.0, the factors a 256 MiB device copy reads (FETCH_SIZE counts
 # half the bytes moved).  Commands and figures in
 # profiles/littlebit_decode_calls.md; a kind without a measurement reports null.
-MEASURED_TRAFFIC = {"qkv": 1_418_656, "o": 694_880, "gate/up": 2_002_528, "down": 1_451_904}
+MEASURED_TRAFFIC = {"qkv": 1_229_984, "o": 616_288, "gate/up": 1_811_040, "down": 1_128_064}
 # the same for the target's calls at M = 8 (profiles/littlebit_verify_m8_target.md)
 MEASURED_TRAFFIC_M8 = {"qkv": 11_636_122, "o": 5_105_971, "gate/up": 17_666_765, "down": 9_626_419}
 MALL_BYTES = 256 << 20
