@@ -517,7 +517,9 @@ def cpu_baseline(layers, budget_s=12.0):
 
     * value: ``littlebit_linear`` (int32-packed signs, int8 activations) over
       whole draft steps, the 224 linears of config 2, in GB/s of the same
-      algorithmic bytes as the GPU value;
+      algorithmic bytes as the GPU value -- the reference's fastest linears
+      on a many-core host (its i2 linears, timed through ``full_forward`` at
+      position 0, run their first stage on one thread);
     * the same op on the 1.0-BPW target's verify linears at M = 8 (both
       branches of every projection; a sample of layers, scaled to 32);
     * ``generate_token``, the reference's fastest CPU draft token (i2 signs,
@@ -601,6 +603,8 @@ def cpu_baseline(layers, budget_s=12.0):
     # --- the reference's decode runtime ------------------------------------------
     H, I, V, HD = 4096, 11008, 32000, 128
     draft_layers, draft_dims = RR.build_layers(ops, H, I, H, {"attn": 205, "mlp": 298}, layers, seed=3)
+    # the runtime's i2 linears: full_forward at position 0 (attention over one position)
+    ff_s, ff_n = RR.time_full_forward(ops, draft_layers, draft_dims, layers, H, V, 32, HD, 0, 600, budget_s * 0.15)
     tok_s, tok_n = RR.time_generate_token(ops, draft_layers, draft_dims, layers, H, V, 32, HD, 512, 600,
                                           budget_s * 0.35)
     torch.set_num_threads(4)
@@ -625,6 +629,11 @@ def cpu_baseline(layers, budget_s=12.0):
             "verify_linears_m8": {"ms_per_pass": round(ms_verify, 2), "gbs": round(vbytes / ms_verify / 1e6, 3),
                                   "sample": f"{vl} layers x 7 projections (draft + residual branch each, summed), "
                                             f"{nv} passes in {elv:.1f} s, scaled to 32 layers"},
+            "draft_step_i2_full_forward": {
+                "ms_per_step": round(ff_s * 1000.0, 3), "gbs": round(step_bytes / ff_s / 1e9, 3), "calls": ff_n,
+                "workload": f"full_forward at position 0: the runtime's {layers} layers of i2 linears (patch:1320-1369; "
+                            "their first stage runs on one thread) with RMSNorms, SiLU * up and residual adds, "
+                            "attention over one position; GB/s on the draft step's algorithmic bytes"},
             "draft_token_generate_token": {
                 "ms_per_token": round(tok_s * 1000.0, 3), "tok_per_s": round(1.0 / tok_s, 2), "tokens": tok_n,
                 "threads_4": {"ms_per_token": round(tok4_s * 1000.0, 3), "tokens": tok4_n},

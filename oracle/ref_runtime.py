@@ -115,6 +115,35 @@ def time_generate_token(ops, layers, dims, n_layers: int, hidden: int, vocab: in
             return el / n, n
 
 
+def time_full_forward(ops, layers, dims, n_layers: int, hidden: int, vocab: int, kv_heads: int, head_dim: int,
+                      position: int, max_seq: int, budget_s: float, seed: int = 1) -> Tuple[float, int]:
+    """Seconds per call of ``full_forward`` (embedding, all layers, final
+    norm; no lm_head) for one token at a fixed ``position``, within a time
+    budget; returns (seconds per call, calls timed).  At position 0 the
+    attention covers one position, so the call is the layers' i2 linears
+    (patch:1320-1369) plus the RMSNorms, SiLU * up and residual adds."""
+    import torch
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    emb = torch.from_numpy(rng.standard_normal((vocab, hidden)).astype(np.float32))
+    norm = torch.from_numpy((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+    kv = kv_caches(n_layers, kv_heads, max_seq, head_dim)
+    scale = head_dim ** -0.5
+
+    def step():
+        ops.full_forward(1, emb, norm, layers, kv, dims, n_layers, hidden, kv_heads,
+                         (hidden // head_dim) // kv_heads, head_dim, max_seq, position, scale, 1e-6)
+
+    step()  # warm
+    t0, n = time.perf_counter(), 0
+    while True:
+        step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 10000:
+            return el / n, n
+
+
 def time_full_forward_batch(ops, layers, dims, n_layers: int, hidden: int, vocab: int, kv_heads: int,
                             head_dim: int, n_tokens: int, start: int, max_seq: int, budget_s: float,
                             seed: int = 2) -> Tuple[float, int]:
