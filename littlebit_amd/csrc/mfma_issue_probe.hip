@@ -12,8 +12,9 @@
 //   ring:    the GEMM mainloop's skeleton without the sign expansion
 //            (ring_kernel below), with and without the A-tile loads.
 //
-// Grids: 256 threads per block, 512 blocks (two waves per SIMD on 256 CUs)
-// and 768 (three; not for ring, whose 64 KB of LDS fit two blocks per CU).
+// Grids: 256 threads per block, 256 blocks (one wave per SIMD on 256 CUs),
+// 512 (two) and 768 (three; not for ring, whose 64 KB of LDS fit two blocks
+// per CU).
 // The valu and lds cases use only registers and LDS; ring reads a 4 MiB
 // buffer, every address inside it.  Each thread stores one float at the end,
 // into a buffer of exactly grid x 256 floats.
@@ -268,6 +269,8 @@ int main() {
     return 1;
   good = good && ring_case<0>(src, out, 512, a, b) && ring_case<1>(src, out, 512, a, b) &&
          ring_case<2>(src, out, 512, a, b);
+  good = good && valu_case<0, false>(out, 256, a, b) && valu_case<4, false>(out, 256, a, b) &&
+         lds_case<1>(out, 256, a, b) && lds_case<2>(out, 256, a, b);  // one wave per SIMD
   for (int blocks : {512, kMaxBlocks}) {
     good = good && valu_case<0, false>(out, blocks, a, b) && valu_case<2, false>(out, blocks, a, b) &&
            valu_case<4, false>(out, blocks, a, b) && valu_case<6, false>(out, blocks, a, b) &&
