@@ -113,7 +113,7 @@ constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) |
 constexpr int kWaitLgkm0 = waitcnt_vm_lgkm0(63);
 constexpr int kSrcTiles = 256;  // 4 MiB of bf16
 
-template <int MODE>
+template <int MODE, int WM = 1>
 __global__ __launch_bounds__(kThreads, 2) void ring_kernel(const uint16_t* __restrict__ src, float* out, int steps) {
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
   typedef __attribute__((address_space(1))) void* glb_ptr_t;
@@ -174,10 +174,17 @@ __global__ __launch_bounds__(kThreads, 2) void ring_kernel(const uint16_t* __res
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 32 * i + lr;  // chunk swizzle of the library's A tiles (no bank conflicts)
-        const u32x4 af = *reinterpret_cast<const u32x4*>(a + r * 64 + (((2 * s + lh) ^ ((r ^ (r >> 3)) & 7)) << 3));
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
-                                                         __builtin_bit_cast(bf16x8, b), acc[i], 0, 0, 0);
+        // WM = 1: the wave's 4 row tiles, one MFMA each; WM = 2: 2 row tiles of
+        // the wave's half of the rows, each A fragment feeding 2 MFMAs
+        if (WM == 1 || i < 2) {
+          const int r = (WM == 1 ? 0 : 64 * (wave >> 1)) + 32 * i + lr;  // library's chunk swizzle
+          const u32x4 af = *reinterpret_cast<const u32x4*>(a + r * 64 + (((2 * s + lh) ^ ((r ^ (r >> 3)) & 7)) << 3));
+#pragma unroll
+          for (int u = 0; u < WM; ++u)
+            acc[WM * i + u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
+                                                                      __builtin_bit_cast(bf16x8, b), acc[WM * i + u],
+                                                                      0, 0, 0);
+        }
       }
   };
   for (int ks = 0; ks + 2 <= steps; ks += 2) {  // steps is even
@@ -237,18 +244,21 @@ bool lds_case(float* out, int blocks, hipEvent_t a, hipEvent_t b) {
   return true;
 }
 
-template <int MODE>
+template <int MODE, int WM = 1>
 bool ring_case(const uint16_t* src, float* out, int blocks, hipEvent_t a, hipEvent_t b) {
   const int steps = 2000;
-  hipLaunchKernelGGL((ring_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
+  hipLaunchKernelGGL((ring_kernel<MODE, WM>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
   if (!ok(hipGetLastError(), "launch") || !ok(hipEventRecord(a), "event")) return false;
-  for (int r = 0; r < 5; ++r) hipLaunchKernelGGL((ring_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
+  for (int r = 0; r < 5; ++r)
+    hipLaunchKernelGGL((ring_kernel<MODE, WM>), dim3(blocks), dim3(kThreads), 0, 0, src, out, steps);
   float ms = 0.f;
   if (!ok(hipEventRecord(b), "event") || !ok(hipEventSynchronize(b), "sync") || !ok(hipEventElapsedTime(&ms, a, b), "t"))
     return false;
   ms /= 5;
   const double mfmas = double(blocks) * (kThreads / 64) * steps * 16;
-  printf("{\"case\": \"ring\", \"a_tiles\": \"%s\", \"blocks\": %d, \"ms\": %.4f, \"tflops\": %.1f}\n",
+  printf("{\"case\": \"ring\", \"waves\": \"%s\", \"a_tiles\": \"%s\", \"blocks\": %d, \"ms\": %.4f, "
+         "\"tflops\": %.1f}\n",
+         WM == 1 ? "1x4 (4 x 1 tiles)" : "2x2 (2 x 2 tiles)",
          MODE == 0 ? "none" : MODE == 1 ? "global_load_lds" : "global_load + ds_write", blocks, ms,
          mfmas * kMfmaFlops / (ms * 1e-3) / 1e12);
   fflush(stdout);
@@ -268,7 +278,8 @@ int main() {
       !ok(hipMemset(src, 0x3F, size_t(kSrcTiles) * kTileElems * sizeof(uint16_t)), "hipMemset"))
     return 1;
   good = good && ring_case<0>(src, out, 512, a, b) && ring_case<1>(src, out, 512, a, b) &&
-         ring_case<2>(src, out, 512, a, b);
+         ring_case<2>(src, out, 512, a, b) && ring_case<0, 2>(src, out, 512, a, b) &&
+         ring_case<1, 2>(src, out, 512, a, b);
   good = good && valu_case<0, false>(out, 256, a, b) && valu_case<4, false>(out, 256, a, b) &&
          lds_case<1>(out, 256, a, b) && lds_case<2>(out, 256, a, b);  // one wave per SIMD
   for (int blocks : {512, kMaxBlocks}) {
