@@ -135,6 +135,89 @@ class DraftStep:
             c.run()
 
 
+class ChainStep:
+    """One replica of a draft step's 224 projections with a decode step's
+    data flow: q/k/v of RMSNorm(x); o of a fixed stand-in for the attention
+    output, added to x (the residual stream); gate/up of RMSNorm(x); down of
+    SiLU(gate) * up, added to x; then the next layer's q/k/v.  ``joined``
+    runs each layer's o, gate/up, down and the next layer's q/k/v as one
+    LittleBitChain (n + 1 launches for n links: 5 per layer); otherwise the
+    same calls one by one (8 per layer).  Every step starts from the same x0
+    (layer 0's o adds into x from x0), so replays repeat exactly."""
+
+    def __init__(self, gen, dev, layers, joined=True):
+        import torch
+        from littlebit_amd import ChainLink, LittleBitChain, LittleBitProjection, LittleBitProjectionGroup
+        from littlebit_amd.synthetic import llama_projection_shapes
+        shapes = {s[0]: s for s in llama_projection_shapes(residual=False)}
+        H, I = shapes["gate_proj"][1], shapes["gate_proj"][2]
+        kv = shapes["k_proj"][2]
+        self.joined = joined
+        self.bytes = self.weight_bytes = 0
+        self.layers = []
+        for _ in range(layers):
+            lp = {}
+            for nm, (_, K, N, ranks) in shapes.items():
+                lp[nm] = LittleBitProjection([make_device_branch(gen, K, R, N, dev) for R in ranks])
+                self.bytes += proj_bytes(1, K, N, ranks)
+                self.weight_bytes += proj_bytes(1, K, N, ranks) - 4 * (K + N)
+            lp["ln1"] = (torch.rand(H, generator=gen) + 0.5).to(dev)
+            lp["ln2"] = (torch.rand(H, generator=gen) + 0.5).to(dev)
+            lp["qkv"] = LittleBitProjectionGroup([lp["q_proj"], lp["k_proj"], lp["v_proj"]])
+            lp["gu"] = LittleBitProjectionGroup([lp["gate_proj"], lp["up_proj"]])
+            self.layers.append(lp)
+        self.x0 = torch.randn((1, H), generator=gen).to(dev)
+        self.a = torch.randn((1, H), generator=gen).to(dev)
+        self.x = torch.empty((1, H), device=dev)
+        self.q, self.k, self.v = (torch.empty((1, n), device=dev) for n in (H, kv, kv))
+        self.g, self.u = (torch.empty((1, I), device=dev) for _ in range(2))
+        self.chains = []
+        if joined:
+            for li, lp in enumerate(self.layers):
+                links = [ChainLink(lp["o_proj"], [self.x], residuals=[self.x0 if li == 0 else self.x]),
+                         ChainLink(lp["gu"], [self.g, self.u], rms_weight=lp["ln2"]),
+                         ChainLink(lp["down_proj"], [self.x], residuals=[self.x], silu_mul=True)]
+                if li + 1 < len(self.layers):
+                    nx = self.layers[li + 1]
+                    links.append(ChainLink(nx["qkv"], [self.q, self.k, self.v], rms_weight=nx["ln1"]))
+                self.chains.append(LittleBitChain(links))
+            assert all(c.fused(self.a) for c in self.chains), "the draft step's chains run joined"
+
+    def run(self):
+        L0 = self.layers[0]
+        L0["qkv"].forward(self.x0, outs=[self.q, self.k, self.v], rms_weight=L0["ln1"])
+        if self.joined:
+            for c in self.chains:
+                c.forward(self.a)
+            return
+        for li, lp in enumerate(self.layers):
+            lp["o_proj"].forward(self.a, out=self.x, residual=self.x0 if li == 0 else self.x)
+            lp["gu"].forward(self.x, outs=[self.g, self.u], rms_weight=lp["ln2"])
+            lp["down_proj"].forward(self.g, out=self.x, residual=self.x, x_up=self.u)
+            if li + 1 < len(self.layers):
+                nx = self.layers[li + 1]
+                nx["qkv"].forward(self.x, outs=[self.q, self.k, self.v], rms_weight=nx["ln1"])
+
+
+def chain_step_bench(gen, dev, stream, layers, steps, warmup):
+    """The decode step's 224 projections with their data flow, joined into
+    chains and one by one, cold (replicas rotated) and warm."""
+    out = {}
+    for joined in (True, False):
+        first = ChainStep(gen, dev, layers, joined)
+        replicas = max(2, math.ceil(2 * MALL_BYTES / first.weight_bytes))
+        reps = [first] + [ChainStep(gen, dev, layers, joined) for _ in range(replicas - 1)]
+        graphs = [capture(r.run, stream) for r in reps]
+        cold = time_graphs(graphs, steps, warmup, stream)
+        warm = time_graphs(graphs[:1], steps, warmup, stream)
+        key = "joined" if joined else "one_by_one"
+        out[key] = {"ms_per_step": round(cold, 4), "warm_ms_per_step": round(warm, 4),
+                    "value": round(first.bytes / (cold * 1e-3) / 1e9, 3), "bytes_per_step": first.bytes,
+                    "replicas": replicas}
+        del graphs, reps, first
+    return out
+
+
 def capture(fn, stream):
     import torch
     g = torch.cuda.CUDAGraph()
@@ -695,7 +778,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
     ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy",
-                                       "lm_head", "small", "handoff", "issue"], default=None,
+                                       "lm_head", "small", "handoff", "issue", "chain"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -746,6 +829,9 @@ def main():
         return
     if args.only in ("decode", "draft"):
         print(json.dumps(decode_bench(dev, target=args.only == "decode")))
+        return
+    if args.only == "chain":
+        print(json.dumps(chain_step_bench(gen, dev, stream, args.layers, args.steps, args.warmup)))
         return
     if args.only == "verify":
         print(json.dumps(verify_linears_bench(gen, dev, stream, args.layers, steps=args.steps, warmup=args.warmup)))

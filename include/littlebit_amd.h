@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LBK_ABI_VERSION 8
+#define LBK_ABI_VERSION 9
 
 /* Element types of activations and outputs. */
 #define LBK_F32 0
@@ -184,6 +184,45 @@ int lbk_group_forward_ex(const lbk_projection* projs, int n_proj, int64_t M,
                          int64_t K, const void* x, int x_dtype,
                          const lbk_input* input, int y_dtype, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* One call of a chain: projections sharing one input (in_features K), and
+ * how they read it (input NULL = plain).  Link 0 reads the chain's x like a
+ * group call (any input kind).  Link j > 0 reads the outputs of link j - 1,
+ * whose out_features must equal K: plain or RMSNORM (rms_weight, rms_eps)
+ * read the y of link j - 1's one projection; SILU_MUL reads
+ * SiLU(y_0) * y_1 of its two (gate, up; input->x1 is ignored). */
+typedef struct lbk_chain_link {
+  const lbk_projection* projs;
+  int n_proj;
+  int64_t in_features;
+  const lbk_input* input;
+} lbk_chain_link;
+
+#define LBK_MAX_CHAIN 8
+
+/* Bytes of workspace lbk_chain_forward uses for these links (0 with the
+ * error set if a link is invalid); one workspace serves chains and every
+ * other call on its stream. */
+size_t lbk_chain_workspace_bytes(const lbk_chain_link* links, int n_links);
+
+/* One row (M = 1, fp32 x and y) through up to LBK_MAX_CHAIN calls in
+ * sequence, each writing every y of its projections (residuals, biases and
+ * input kinds as in lbk_group_forward_ex): the same as calling
+ * lbk_group_forward_ex link by link, in n_links + 1 launches instead of
+ * 2 n_links -- each kernel between two links expands link j's rows and adds
+ * their part of link j + 1's latent vector while they are still on chip.
+ * The reference runs a decoder layer's projections (o, gate/up, down, and
+ * the next layer's q/k/v) in one call, patches/littlebit_cpu_optimized.cpp:
+ * 1627-1833 (full_forward).  Under lbk_set_deterministic(1), or for shapes
+ * the joined kernel does not take (lbk_chain_fused), the links run as
+ * separate calls with the same results. */
+int lbk_chain_forward(const lbk_chain_link* links, int n_links, const void* x, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* 1 if lbk_chain_forward would run these links joined, 0 if as separate
+ * calls, a negative LBK_ERR_* code if they are invalid.  No counterpart in
+ * the reference (a launch-plan query). */
+int lbk_chain_fused(const lbk_chain_link* links, int n_links, const void* x);
 
 /* Bytes of the device scratch lbk_group_forward_noalloc works in. */
 #define LBK_NOALLOC_SCRATCH_BYTES (8u << 20)

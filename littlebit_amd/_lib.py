@@ -76,11 +76,23 @@ class LbkInput(ctypes.Structure):
     ]
 
 
+class LbkChainLink(ctypes.Structure):
+    """Mirror of ``lbk_chain_link``."""
+
+    _fields_ = [
+        ("projs", ctypes.POINTER(LbkProjection)),
+        ("n_proj", ctypes.c_int),
+        ("in_features", ctypes.c_int64),
+        ("input", ctypes.POINTER(LbkInput)),
+    ]
+
+
 LBK_INPUT_PLAIN = 0
 LBK_INPUT_RMSNORM = 1
 LBK_INPUT_SILU_MUL = 2
 LBK_INPUT_ATTN_MERGE = 3
 LBK_MAX_GROUP = 4
+LBK_MAX_CHAIN = 8
 LBK_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 # name -> (restype, argtypes); must list every function of include/littlebit_amd.h
@@ -112,6 +124,12 @@ SIGNATURES = {
         [ctypes.POINTER(LbkProjection), ctypes.c_int, _I64, _I64, _VP, ctypes.c_int, ctypes.POINTER(LbkInput),
          ctypes.c_int, _VP],
     ),
+    "lbk_chain_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(LbkChainLink), ctypes.c_int]),
+    "lbk_chain_forward": (
+        ctypes.c_int,
+        [ctypes.POINTER(LbkChainLink), ctypes.c_int, _VP, _VP, ctypes.c_size_t, _VP],
+    ),
+    "lbk_chain_fused": (ctypes.c_int, [ctypes.POINTER(LbkChainLink), ctypes.c_int, _VP]),
     "lbk_littlebit_linear": (
         ctypes.c_int,
         [_VP, _I64, _VP, _VP, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, ctypes.c_size_t, _VP],

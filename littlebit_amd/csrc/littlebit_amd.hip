@@ -251,6 +251,15 @@ struct MfmaParams {
   // half.  Null otherwise (partials meet in fp32 atomics, in no fixed order).
   float* part;
   uint32_t* det_cnt;
+  // Chains (one row, see chain_mfma_kernel): explicit latent regions instead
+  // of the halves.  tdst set: the latent kernel accumulates t (and the sums
+  // of squares at tdst + tsize) there and leaves the halves' state alone;
+  // tsrc set: the expand kernel reads t there and leaves the state alone.
+  // Either kernel then clears clr[0, nclr), spread over its blocks.
+  float* tdst;
+  const float* tsrc;
+  float* clr;
+  int nclr;
 };
 
 // Latent buffer protocol (all writes idempotent, so no ordering between
@@ -851,8 +860,9 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
     // RMSNorm: t is accumulated without the rows' 1/rms; the blocks of the
     // first row-block add their chunk's sums of squares next to t, and the
     // expand kernel scales t by 1/rms when it stages it
-    float* ssq_out = p.part ? p.part + size_t(p.nkc) * p.tsize + size_t(2 * kc) * kMaxMfmaM
-                            : p.t2 + size_t(h) * kTHalf + p.tsize + mrow0;
+    float* ssq_out = p.part   ? p.part + size_t(p.nkc) * p.tsize + size_t(2 * kc) * kMaxMfmaM
+                     : p.tdst ? p.tdst + p.tsize + mrow0
+                              : p.t2 + size_t(h) * kTHalf + p.tsize + mrow0;
     if (MT == 1 && p.xmode == LBK_INPUT_ATTN_MERGE) {
       if constexpr (MT == 1) stage_latent_attn<NCH>(p, g, k0, lds_a, tid);
     } else if (p.xmode == LBK_INPUT_RMSNORM)
@@ -902,7 +912,7 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum[mb][i] = acc[mb][i] + __shfl_xor(acc[mb][i], 32);
 
-  float* trow = p.t2 + size_t(h) * kTHalf + tb + r;
+  float* trow = (p.tdst ? p.tdst : p.t2 + size_t(h) * kTHalf) + tb + r;
   if constexpr (DET) {
     // Deterministic mode: this k-chunk's partials go to part[kc] through
     // agent-scope stores (the row-block's blocks run on any XCD); once they
@@ -1033,7 +1043,12 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
   // clear this block's slice of the other half; publish the state
   const int nblk = int(gridDim.x * gridDim.y);
   const int bl = int(blockIdx.x + blockIdx.y * gridDim.x);
-  {
+  if (p.tdst) {
+    // a chain's first call: its own region, and the region given to clear
+    const int per = (p.nclr + nblk - 1) / nblk;
+    const int hi = min(p.nclr, (bl + 1) * per);
+    for (int i = bl * per + tid; i < hi; i += kBlock) p.clr[i] = 0.f;
+  } else {
     const uint32_t stale = h ? s0 : s1;
     float* __restrict__ other = p.t2 + size_t(h ^ 1u) * kTHalf;
     const int per = int((stale + unsigned(nblk) - 1) / unsigned(nblk));
@@ -1218,10 +1233,20 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
   const int ng = (nsteps + 3) / 4;
   const int sb0 = min(4 * (int(blockIdx.y) * ng / ks), nsteps);
   const int sb1 = min(4 * ((int(blockIdx.y) + 1) * ng / ks), nsteps);
-  const uint32_t hq = __builtin_amdgcn_readfirstlane(hq_word) & 1u;
-  // block (0, 0, 0) hands the latent buffer on (P = 1 - Q), before any return
-  if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0)
+  // (a chain's last call does not wait for the word)
+  const uint32_t hq = p.tsrc ? 0u : __builtin_amdgcn_readfirstlane(hq_word) & 1u;
+  if (p.tsrc) {
+    // a chain's last call: t from its region; every block clears its share
+    // of the region given to clear
+    const int nblk = int(gridDim.x * gridDim.y * gridDim.z);
+    const int bl = int(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+    const int per = (p.nclr + nblk - 1) / nblk;
+    const int hi = min(p.nclr, (bl + 1) * per);
+    for (int i = bl * per + tid; i < hi; i += THREADS) p.clr[i] = 0.f;
+  } else if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && tid == 0) {
+    // block (0, 0, 0) hands the latent buffer on (P = 1 - Q), before any return
     __hip_atomic_store(p.sync, hq ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (sb0 >= sb1 || int(blockIdx.x) >= p.ntiles) return;
   // parts of a two-branch sequence start at multiples of 4 (no group spans P0)
   const int len = sb1 - sb0;
@@ -1240,7 +1265,7 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
   const int c1a = two ? 16 * min(max(sb0 - sq.P0, 0), sq.steps[1]) : 0;
   const int nch1 = two ? 16 * min(max(sb1 - sq.P0, 0), sq.steps[1]) - c1a : 0;
   const int nch = nch0 + nch1;
-  const float* __restrict__ ta = p.t2 + size_t(hq) * kTHalf;
+  const float* __restrict__ ta = p.tsrc ? p.tsrc : p.t2 + size_t(hq) * kTHalf;
   const float* __restrict__ tssq = ta + p.tsize + mrow0;  // the chunk's rows' sums of squares
   u32x4* tb0 = lds_t;
   u32x4* tb1 = lds_t + size_t(L::MB) * nch0 * L::ROWS;
@@ -1507,6 +1532,386 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
           const int m = mb * 8 + grp * 4 + i;
           if (m < M) store_out(y, size_t(mrow0 + m) * N + n, out[mb][i] + bn + (P.res ? resv[mb][i] : 0.f));
         }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chains (one row, fp32): calls ("links") each of which reads the outputs of
+// the link before it -- o, gate/up, down and the next layer's q/k/v of a
+// decode step, which the reference runs as one call per layer with thread
+// barriers between its stages (patches/littlebit_cpu_optimized.cpp:
+// 1627-1833).  The latent stage of link j + 1 sums over its input's k; the
+// k-chunk [c0, c0 + C) of that input is rows [c0, c0 + C) of link j's
+// outputs.  So one kernel does both: a block expands C = 16 W output rows of
+// the NT projections of link j that link j + 1 reads (gate and up for SiLU *
+// up, else the one projection) and, with those rows still in registers, adds
+// the k-chunk's part of link j + 1's latent vector into its region with fp32
+// atomics.  A chain of n links takes n + 1 launches: link 0's latent kernel,
+// n - 1 of these, link n - 1's expand kernel (two per link otherwise).
+//
+// Latent regions (kChainRegion floats each, one row: t of every branch, then
+// the sum of squares of an RMSNorm input): link 0's latent kernel fills
+// region 0 and clears the last region (kChainLast, left by the final expand
+// of the chain before); the kernel joining links j and j + 1 reads region j,
+// fills region j + 1 (the last region when j + 1 = n - 1) and clears region
+// j - 1, which the kernel before it read; the final expand reads the last
+// region and clears region n - 2.  No kernel clears a region another kernel
+// of the chain still reads or fills, and every region but the last is zero
+// again when a chain ends, whatever its length.
+// ---------------------------------------------------------------------------
+constexpr int kMaxChainLinks = 8;
+constexpr int kChainRegion = int(kMaxRankTotal) + kMaxSeg * 128 + kSsqSlots;  // floats
+constexpr int kChainLast = kMaxChainLinks - 1;  // index of the last region
+static_assert(kChainRegion % 64 == 0, "regions keep 256-byte alignment");
+
+// The joined kernel's arguments, compact: every kernel-argument cache line a
+// kernel touches first costs a memory round trip, and two full MfmaParams
+// (about 2 KB, reached in dependent steps) cost several.
+struct ChainProj {  // a projection of link j, as the joined kernel expands it
+  const uint32_t* U[2];
+  const float* h[2];
+  const float* bias;
+  const float* res;
+  float* y;
+  int RW[2];
+  int steps[2];  // rank steps (4 sign words each) per branch
+  int tbase[2];
+  int nb;
+  int pad;
+};
+struct ChainSeg {  // a segment (branch) of link j + 1, as the joined kernel reads it
+  const uint32_t* vt;  // V's tiled copy
+  const float* l;
+  const float* g;
+  int R;
+  int tbase;
+};
+struct ChainParams {
+  const float* tsrc;  // link j's t, then its sum of squares at tsrc + tsize_e
+  float* tdst;        // link j + 1's t, then its sum of squares at tdst + tsize_l
+  const float* nw;    // link j + 1's RMSNorm weight
+  float* clr;         // cleared here, spread over the blocks
+  int tsize_e, late, Ke, N;  // link j: t floats, 1/rms deferred to here, K, outputs
+  float eps;
+  int nseg, Kl, KWl, xmode, tsize_l, nclr, pad;  // link j + 1
+  ChainProj proj[2];
+  ChainSeg seg[kMaxSeg];
+};
+
+// grid = ceil(N / C) blocks of W waves; wave w expands rows c0 + 16 w .. + 15
+// of each projection p < NT (all of its rank steps, both branches), lanes
+// 0..15 ending with y of row c0 + 16 w + lane.  LDS: link j's t (compact,
+// per projection and branch, 16 chunks of 8 ranks per step), then link
+// j + 1's A operand per segment (NCH chunks).
+template <int S, int W, int NT>
+__global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
+  using L = Compact<1>;
+  constexpr int THREADS = W * kWave;
+  constexpr int C = 16 * W;   // rows of link j per block = k-chunk of link j + 1
+  constexpr int NCH = C / 8;  // 8-column chunks of the k-chunk
+  constexpr int NVW = C / 32; // V words per latent row of the k-chunk
+  // latent tiles per wave whose V words are in flight at once (16-32 VGPRs)
+  constexpr int TPW = NVW <= 4 ? 8 : 2;
+  static_assert(NT == 1 || NT == 2, "one projection, or gate and up");
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+  u32x4* lds = reinterpret_cast<u32x4*>(lds_raw);
+  __shared__ float xs[C];
+  __shared__ float ssqw[W];
+  const int tid = int(threadIdx.x);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int c0 = int(blockIdx.x) * C;
+  // link j + 1's latent stage: wave w takes segment w % nseg (nseg <= W),
+  // and of its 16-row tiles those k with k % nws == w / nseg, nws the waves
+  // of that segment; the A operand of segment w is built by wave w.  The
+  // segment's fields are read here, so that their round trip overlaps the
+  // issue of the loads below.
+  const int nseg = cp.nseg;
+  const int ws = wave % nseg;
+  const int wi = wave / nseg;
+  const int nws = (W - ws + nseg - 1) / nseg;
+  const ChainSeg& G = cp.seg[ws];
+  const int ntile = (G.R + 15) >> 4;
+  const int N = cp.N;
+  const int n = c0 + 16 * wave + col;
+  const bool nvalid = n < N;
+  const int nc = nvalid ? n : 0;
+
+  // link j's step sequences and staged chunks, (projection, branch) in order
+  // (no local array is indexed per lane below: the compiler would keep it in
+  // scratch memory)
+  StepSeq sq[NT];
+  int nchb[2 * NT], cb[2 * NT], tbb[2 * NT];
+  int ntask = 0;
+#pragma unroll
+  for (int q = 0; q < NT; ++q) {
+    const ChainProj& P = cp.proj[q];
+    const bool two = P.nb > 1;
+    sq[q].U[0] = P.U[0];
+    sq[q].U[1] = P.U[two ? 1 : 0];
+    sq[q].RW[0] = P.RW[0];
+    sq[q].RW[1] = P.RW[two ? 1 : 0];
+    sq[q].steps[0] = P.steps[0];
+    sq[q].steps[1] = P.steps[two ? 1 : 0];
+    sq[q].P0 = two ? (sq[q].steps[0] + 3) & ~3 : sq[q].steps[0];
+    sq[q].N = N;
+    nchb[2 * q] = 16 * sq[q].steps[0];
+    nchb[2 * q + 1] = two ? 16 * sq[q].steps[1] : 0;
+    tbb[2 * q] = P.tbase[0];
+    tbb[2 * q + 1] = P.tbase[two ? 1 : 0];
+    cb[2 * q] = ntask;
+    ntask += nchb[2 * q];
+    cb[2 * q + 1] = ntask;
+    ntask += nchb[2 * q + 1];
+  }
+  const float* __restrict__ ta = cp.tsrc;
+
+  // (1) staging loads of the thread's first task (chunk h: 8 ranks of t)
+  const int cb1 = cb[1], tb0 = tbb[0], tb1 = tbb[1];
+  const int cb2 = NT == 2 ? cb[2 % (2 * NT)] : ntask, cb3 = NT == 2 ? cb[3 % (2 * NT)] : ntask;
+  const int tb2 = NT == 2 ? tbb[2 % (2 * NT)] : 0, tb3 = NT == 2 ? tbb[3 % (2 * NT)] : 0;
+  auto src_of = [&](int h) {
+    // chunk h - cb[i] of piece i starts at tbb[i] + 8 (h - cb[i])
+    const int base = h < cb1 ? tb0 : h < cb2 ? tb1 - 8 * cb1 : h < cb3 ? tb2 - 8 * cb2 : tb3 - 8 * cb3;
+    return ta + base + 8 * h;
+  };
+  float4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+  if (tid - lane < ntask) {
+    const float* s0 = src_of(min(tid, ntask - 1));
+    v0 = *reinterpret_cast<const float4*>(s0);
+    v1 = *reinterpret_cast<const float4*>(s0 + 4);
+  }
+  const bool late = cp.late != 0;
+  // a vector load (index opaque to the compiler): a scalar one would make
+  // every later wait for the kernel arguments wait for it too
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const float ssq = late ? ta[cp.tsize_e + zero] : 0.f;
+  auto put = [&](int h, float4 a0, float4 a1, float r) {
+    const float a[8] = {a0.x * r, a0.y * r, a0.z * r, a0.w * r, a1.x * r, a1.y * r, a1.z * r, a1.w * r};
+    u32x4 hi, lo;
+    split8(a, hi, lo);
+    u32x4* base = lds + size_t(h) * L::ROWS;
+    base[0] = hi;
+    base[1] = lo;
+    base[2] = u32x4{0u, 0u, 0u, 0u};
+  };
+  float rs = 1.f;
+  // more chunks than threads: all staged here, before the sign words are
+  // issued (a loop of loads and waits after them would wait for them too)
+  const bool tail = ntask > THREADS;  // block-uniform
+  if (tail) {
+    if (late) rs = inv_rms(ssq, 1.f / float(cp.Ke), cp.eps);
+    if (tid < ntask) put(tid, v0, v1, rs);
+    for (int h = tid + THREADS; h < ntask; h += THREADS) {
+      const float* s = src_of(h);
+      put(h, *reinterpret_cast<const float4*>(s), *reinterpret_cast<const float4*>(s + 4), rs);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // (2) sign words of the wave's rows, every step of each projection
+  SignWords<S> sw[NT];
+#pragma unroll
+  for (int q = 0; q < NT; ++q) sw[q].load(sq[q], nc, 0, sq[q].P0 + (cp.proj[q].nb > 1 ? sq[q].steps[1] : 0), grp);
+  // (3) epilogue operands of link j
+  float h0v[NT], h1v[NT], bnv[NT], resv[NT];
+#pragma unroll
+  for (int q = 0; q < NT; ++q) {
+    const ChainProj& P = cp.proj[q];
+    h0v[q] = P.h[0][nc];
+    h1v[q] = P.nb > 1 ? P.h[1][nc] : 0.f;
+    bnv[q] = P.bias ? P.bias[nc] : 0.f;
+    resv[q] = P.res ? P.res[nc] : 0.f;
+  }
+  // (4) link j + 1's latent stage (its segment's fields were read first)
+  const int kw0 = c0 / 32;
+  const int kw4 = (cp.KWl + 3) >> 2;
+  // V words of the k-chunk for the lane's row of the wave's k-th tile, from
+  // V's tiled copy [ceil(R/16)][ceil(KW/4)][16 rows][4 words] (whole 16-byte
+  // cells), and l of the row
+  auto load_vw = [&](int k, uint32_t (&w)[NVW], float& lv) {
+    const int t = min(wi + k * nws, ntile - 1);
+    const int r = 16 * t + col;
+    const int rr = r < G.R ? r : 0;
+    lv = G.l[rr];
+    const uint32_t* __restrict__ cells = G.vt + size_t(rr >> 4) * kw4 * 64 + (rr & 15) * 4;
+    if constexpr (NVW == 2) {
+      const int gi = kw0 < cp.KWl ? kw0 >> 2 : 0;
+      const uint2 v = *reinterpret_cast<const uint2*>(cells + size_t(gi) * 64 + (kw0 & 3));
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
+#pragma unroll
+      for (int q = 0; q < NVW / 4; ++q) {
+        const int gi = (kw0 >> 2) + q < kw4 ? (kw0 >> 2) + q : 0;
+        const uint4 v = *reinterpret_cast<const uint4*>(cells + size_t(gi) * 64);
+        w[4 * q] = v.x;
+        w[4 * q + 1] = v.y;
+        w[4 * q + 2] = v.z;
+        w[4 * q + 3] = v.w;
+      }
+    }
+  };
+  // g of the A operand (lanes < NCH one 8-column chunk each; masked where
+  // used: a use here would wait for every load issued before it), before
+  // the V words, which the A operand's wait then does not cover
+  const int ac = lane;
+  const int ak = c0 + 8 * ac;
+  const bool gin = wave < nseg && ac < NCH && ak < cp.Kl;  // K % 8 == 0: wholly inside or past K
+  Raw8<float> g8;
+  g8.load(G.g + (gin ? ak : 0));
+  // the V words of the wave's first TPW tiles: one round trip for them all
+  uint32_t vw[TPW][NVW];
+  float lv[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) load_vw(i, vw[i], lv[i]);
+  const float nwv = cp.xmode == LBK_INPUT_RMSNORM ? cp.nw[nc] : 1.f;
+  // (5) the region this launch clears
+  {
+    const int nblk = int(gridDim.x), bl = int(blockIdx.x);
+    const int per = (cp.nclr + nblk - 1) / nblk;
+    const int hi = min(cp.nclr, (bl + 1) * per);
+    for (int i = bl * per + tid; i < hi; i += THREADS) cp.clr[i] = 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!tail) {
+    if (late) rs = inv_rms(ssq, 1.f / float(cp.Ke), cp.eps);
+    if (tid < ntask) put(tid, v0, v1, rs);
+  }
+  __syncthreads();
+
+  // (6) expand: y of the lane's row for each projection
+  uint32_t kmask = 0x80008000u, kone = 0x3F803F80u;
+  asm volatile("" : "+v"(kmask), "+v"(kone));
+  const int lrow = L::lane_row(col);
+  float y[NT];
+#pragma unroll
+  for (int q = 0; q < NT; ++q) {
+    const u32x4* __restrict__ tb0 = lds + size_t(cb[2 * q]) * L::ROWS;
+    const u32x4* __restrict__ tb1 = lds + size_t(cb[2 * q + 1]) * L::ROWS;
+    const bool two = cp.proj[q].nb > 1;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc0 = {0.f, 0.f, 0.f, 0.f};
+    bool in1 = false;
+    auto enter = [&](bool b1) {
+      if (b1 && !in1) {
+        acc0 = acc;
+        acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        in1 = true;
+      }
+    };
+    auto mfma4 = [&](uint32_t word, const u32x4* __restrict__ tb, int w, uint32_t km, uint32_t ko) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 bop = signs_to_bf16x8(word, j, km, ko);
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, tb[(4 * w + j) * L::ROWS + lrow]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc, 0, 0, 0);
+      }
+    };
+    const int nst = sq[q].P0 + (two ? sq[q].steps[1] : 0);
+    const int G = nst >> 2, rem = nst & 3;
+#pragma unroll
+    for (int t = 0; t < S / 4; ++t) {
+      if (t >= G) continue;
+      const bool b1 = 4 * t >= sq[q].P0;
+      enter(b1);
+      uint32_t w4[4];
+      sw[q].group(t, w4);
+      // steps in branch 0's padding get a zero B operand
+      const int st = (b1 ? 4 * t - sq[q].P0 : 4 * t) + grp;
+      const bool valid = b1 || st < sq[q].steps[0];
+      const int sv = valid ? st : 0;
+      const uint32_t km = valid ? kmask : 0u, ko = valid ? kone : 0u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mfma4(w4[u], b1 ? tb1 : tb0, 4 * sv + u, km, ko);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i >= rem) continue;
+      const int qs = 4 * G + i;
+      const bool b1 = qs >= sq[q].P0;
+      enter(b1);
+      mfma4(sw[q].rem[i], b1 ? tb1 : tb0, 4 * (b1 ? qs - sq[q].P0 : qs) + grp, kmask, kone);
+    }
+    if (!in1) {
+      acc0 = acc;
+      acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // C row 0 (lanes 0..15) is hi of the row, C row 8 (lanes 32..47) lo
+    const float s0 = acc0[0] + __shfl_xor(acc0[0], 32);
+    const float s1 = acc[0] + __shfl_xor(acc[0], 32);
+    y[q] = h0v[q] * s0 + h1v[q] * s1 + bnv[q] + resv[q];
+  }
+  // (7) link j's outputs, and link j + 1's input at k = n
+  float xv = 0.f;
+  if (lane < 16) {
+#pragma unroll
+    for (int q = 0; q < NT; ++q)
+      if (nvalid) cp.proj[q].y[n] = y[q];
+    if (nvalid) {
+      if constexpr (NT == 2) xv = silu_f(y[0]) * y[1];
+      else xv = cp.xmode == LBK_INPUT_RMSNORM ? y[0] * nwv : y[0];
+    }
+    xs[16 * wave + col] = xv;
+  }
+  if (cp.xmode == LBK_INPUT_RMSNORM) {
+    // the rows' sum of squares: lanes 0..15 of each wave, then the block
+    float q2 = lane < 16 && nvalid ? y[0] * y[0] : 0.f;
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) q2 += __shfl_xor(q2, o);
+    if (lane == 0) ssqw[wave] = q2;
+  }
+  __syncthreads();
+  if (cp.xmode == LBK_INPUT_RMSNORM && tid == 0) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) s += ssqw[w];
+    unsafeAtomicAdd(cp.tdst + cp.tsize_l, s);
+  }
+  // (8) A operand of link j + 1: hi / lo of g[k] * x[k], segment w by wave w
+  u32x4* lds_a = lds + size_t(ntask) * L::ROWS;
+  if (wave < nseg && ac < NCH) {
+    float gv[8], a[8];
+    g8.get(gv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = gv[e] * xs[8 * ac + e];
+    if (!gin) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = 0.f;
+    }
+    u32x4 hi, lo;
+    split8(a, hi, lo);
+    u32x4* base = lds_a + size_t(wave * NCH + ac) * L::ROWS;
+    base[0] = hi;
+    base[1] = lo;
+    base[2] = u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  // (9) the wave's latent tiles in batches of TPW: NVW MFMAs each over the
+  // k-chunk, then one fp32 atomic per latent row
+  for (int k0 = 0; k0 * nws + wi < ntile; k0 += TPW) {
+    if (k0 > 0) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) load_vw(k0 + i, vw[i], lv[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int t = wi + (k0 + i) * nws;
+      if (t >= ntile) continue;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NVW; ++kk) {
+        const bf16x8 bop = signs_to_bf16x8(vw[i][kk], grp, kmask, kone);
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, lds_a[(size_t(ws) * NCH + 4 * kk + grp) * L::ROWS + lrow]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc, 0, 0, 0);
+      }
+      const float sum = acc[0] + __shfl_xor(acc[0], 32);
+      const int r = 16 * t + col;
+      if (lane < 16 && r < G.R) unsafeAtomicAdd(cp.tdst + G.tbase + r, lv[i] * sum);
     }
   }
 }
@@ -3090,11 +3495,17 @@ int validate_group(const ProjDesc* pd, int np, int64_t M, int64_t K) {
 //   [kDetCntOffset, + 4 kDetMaxBlocks) deterministic mode's row-block counters (zero
 //                                      between calls)
 //   [kTOffset, kTOffset + kTBytes)     MFMA-path latent halves
-//   [kGemmOffset, ...)                 GEMM-path A and T planes, then the
-//                                      stream-K partial tiles (kSkPartBytes)
+//   [kChainOffset, + kChainBytes)      chains' latent regions (zero between
+//                                      chains but for the last region)
+//   [kGemmOffset, ...)                 one call's own scratch: GEMM-path A and
+//                                      T planes, then the stream-K partial
+//                                      tiles (kSkPartBytes); or deterministic
+//                                      mode's partial sums
 constexpr size_t kTOffset = 4096;
 constexpr size_t kTBytes = 2 * size_t(kTHalf) * sizeof(float);
-constexpr size_t kGemmOffset = kTOffset + kTBytes;
+constexpr size_t kChainOffset = kTOffset + kTBytes;
+constexpr size_t kChainBytes = size_t(kMaxChainLinks) * kChainRegion * sizeof(float);
+constexpr size_t kGemmOffset = kChainOffset + kChainBytes;
 static_assert(kCounterBytes <= kTOffset, "counter region overlaps t");
 constexpr int kNumCUs = 256;                   // MI355X
 constexpr int kSkMaxBlocks = 2 * kNumCUs;      // stream-K blocks: two resident per CU (bf16 stage ring)
@@ -3405,7 +3816,7 @@ Plan plan_one(const ProjDesc* pd, int np, int64_t M, int64_t K, bool allow_ks, b
     pl.ks = ex.ks;
     pl.ws_total = pl.ws_min = kTOffset + kTBytes;
     if (det && pl.nkc > 1)
-      pl.ws_total = pl.ws_min = kTOffset + kTBytes + align256(det_part_floats(pd, np, M, pl.nkc) * sizeof(float));
+      pl.ws_total = pl.ws_min = kGemmOffset + align256(det_part_floats(pd, np, M, pl.nkc) * sizeof(float));
   } else {
     pl.ws_min = kGemmOffset + gemm_ws_bytes(pd, np, M, K, true);
     const int64_t tiles = ceil_div(M, kGB) * latent_col_tiles(pd, np), nks = ceil_div(K, kGK);
@@ -3518,10 +3929,11 @@ void dispatch_expand(const MfmaParams& p, const Plan& pl, dim3 grid, hipStream_t
   }
 }
 
-int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
-                 const InputDesc& in, int y_dtype, void* workspace, hipStream_t s) {
+// Kernel parameters of a decode-path call (both of its launches read them);
+// `tiles` = the expand kernel's row tiles.
+int build_mfma_params(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x,
+                      const InputDesc& in, void* workspace, MfmaParams& p, int& tiles) {
   const int rows = 16 * (pl.waves / pl.splits);
-  MfmaParams p;
   memset(&p, 0, sizeof(p));
   p.nproj = np;
   p.splits = pl.splits;
@@ -3583,7 +3995,6 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   // rows past the plan's tile (a call planned in row chunks): the chunks run
   // side by side in the same two launches
   p.crows = pl.chunk > 0 ? pl.chunk : int(M);
-  const int nchunks = int(ceil_div(M, p.crows));
   p.x = x;
   p.wvec = wvec && p.KW % std::max(pl.wpl, 4) == 0 ? 1 : 0;
   p.xvec = xvec ? 1 : 0;
@@ -3595,20 +4006,30 @@ int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t 
   p.t2 = reinterpret_cast<float*>(ws + kTOffset);
   // the plan sized the workspace for the partials when the mode was on
   const bool det = pl.det && pl.nkc > 1 && pl.ws_min > kTOffset + kTBytes;
-  p.part = det ? reinterpret_cast<float*>(ws + kTOffset + kTBytes) : nullptr;
+  p.part = det ? reinterpret_cast<float*>(ws + kGemmOffset) : nullptr;
   p.det_cnt = det ? reinterpret_cast<uint32_t*>(ws + kDetCntOffset) : nullptr;
+  p.ntiles = tile;
+  tiles = tile;
+  return LBK_OK;
+}
 
+int forward_mfma(const ProjDesc* pd, int np, const Plan& pl, int64_t M, int64_t K, const void* x, int x_dtype,
+                 const InputDesc& in, int y_dtype, void* workspace, hipStream_t s) {
+  MfmaParams p;
+  int tile = 0;
+  int rc = build_mfma_params(pd, np, pl, M, K, x, in, workspace, p, tile);
+  if (rc != LBK_OK) return rc;
+  const int nchunks = int(ceil_div(M, p.crows));
   const dim3 grid1(unsigned(pl.nrb * pl.nkc), unsigned(nchunks));
   if (x_dtype == LBK_F32) dispatch_latent<float>(p, pl, grid1, s);
   else dispatch_latent<uint16_t>(p, pl, grid1, s);
-  int rc = check_launch("latent_mfma_kernel");
+  rc = check_launch("latent_mfma_kernel");
   if (rc != LBK_OK) return rc;
 
   // With slices, grid.x is padded to a multiple of the 8 XCDs (blocks are
   // dealt to the XCDs in turn by linear index), so that every slice of a
   // row tile runs on one XCD: U rows cut between slices share 128-byte lines,
   // which one L2 then fetches once instead of once per slice's XCD.
-  p.ntiles = tile;
   const dim3 grid2(unsigned(pl.ks > 1 ? (tile + 7) / 8 * 8 : tile), unsigned(pl.ks), unsigned(nchunks));
   if (y_dtype == LBK_F32) dispatch_expand<float>(p, pl, grid2, s);
   else dispatch_expand<uint16_t>(p, pl, grid2, s);
@@ -3930,6 +4351,245 @@ int forward_group(const ProjDesc* pd, int np, int64_t M, int64_t K, const void* 
 }
 
 // ---------------------------------------------------------------------------
+// Chains on the host (see chain_mfma_kernel)
+// ---------------------------------------------------------------------------
+struct ChainLinkDesc {
+  ProjDesc pd[kMaxProj];
+  int np;
+  int64_t K;
+  const void* x;  // link 0: the caller's input; then projection 0's y of the link before
+  InputDesc in;
+  Plan pl;
+};
+
+template <int S, int W, int NT>
+void launch_chain(const ChainParams& cp, unsigned blocks, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((chain_mfma_kernel<S, W, NT>), dim3(blocks), dim3(W * kWave), lds, s, cp);
+}
+template <int S, int W>
+void dispatch_chain_nt(const ChainParams& cp, int nt, unsigned blocks, size_t lds, hipStream_t s) {
+  if (nt == 2) launch_chain<S, W, 2>(cp, blocks, lds, s);
+  else launch_chain<S, W, 1>(cp, blocks, lds, s);
+}
+template <int S>
+void dispatch_chain_w(const ChainParams& cp, int w, int nt, unsigned blocks, size_t lds, hipStream_t s) {
+  (void)w;  // chain_waves: 8
+  dispatch_chain_nt<S, 8>(cp, nt, blocks, lds, s);
+}
+void dispatch_chain(const ChainParams& cp, int steps, int w, int nt, unsigned blocks, size_t lds, hipStream_t s) {
+  switch (steps) {
+    case 4: dispatch_chain_w<4>(cp, w, nt, blocks, lds, s); break;
+    case 8: dispatch_chain_w<8>(cp, w, nt, blocks, lds, s); break;
+    default: dispatch_chain_w<16>(cp, w, nt, blocks, lds, s); break;
+  }
+}
+
+constexpr int kChainMaxSteps = 16;  // rank steps of a joined link's projection (both branches)
+
+// Waves of the kernel joining a link with N outputs to the next: 16 W rows
+// per block, so N / (16 W) blocks each add one partial latent vector.  At
+// one row its waves are bound by their own instruction streams, so two per
+// SIMD on more CUs beat four per SIMD on fewer (draft step 1.085 -> 1.049 ms
+// against 16 waves above 8192 outputs; 4 waves: 1.171 ms).
+int chain_waves(int64_t) { return 8; }
+
+// Latent floats of a link at one row (every branch's RP), as build_mfma_params lays them out.
+int64_t chain_tsize(const ProjDesc* pd, int np) {
+  int64_t t = 0;
+  for (int q = 0; q < np; ++q)
+    for (int b = 0; b < pd[q].nb; ++b) t += 32 * ceil_div(ceil_div(pd[q].br[b].rank, 32), 4) * 4;
+  return t;
+}
+
+// Validation and plans of a chain; `fused` tells whether it runs as one
+// kernel per link boundary (else every link runs as its own call).
+int prepare_chain(const lbk_chain_link* links, int n, const void* x, ChainLinkDesc* cl, bool& fused) {
+  if (!links || n < 1 || n > kMaxChainLinks)
+    return set_error(LBK_ERR_ARG, "n_links must be in [1, %d] with a non-NULL array, got %d", kMaxChainLinks, n);
+  for (int j = 0; j < n; ++j) {
+    const lbk_chain_link& lk = links[j];
+    ChainLinkDesc& c = cl[j];
+    if (!lk.projs || lk.n_proj < 1 || lk.n_proj > kMaxProj)
+      return set_error(LBK_ERR_ARG, "link %d: n_proj must be in [1, %d] with a non-NULL array, got %d", j, kMaxProj,
+                       lk.n_proj);
+    c.np = lk.n_proj;
+    c.K = lk.in_features;
+    for (int q = 0; q < c.np; ++q)
+      c.pd[q] = ProjDesc{lk.projs[q].branches, lk.projs[q].n_branches, lk.projs[q].out_features, lk.projs[q].bias,
+                         lk.projs[q].y, lk.projs[q].residual};
+    lbk_input inp{};
+    inp.kind = LBK_INPUT_PLAIN;
+    if (lk.input) inp = *lk.input;
+    c.x = x;
+    if (j > 0) {
+      const ChainLinkDesc& pv = cl[j - 1];
+      if (inp.kind == LBK_INPUT_SILU_MUL) {
+        if (pv.np != 2)
+          return set_error(LBK_ERR_ARG, "link %d reads SiLU(gate) * up: link %d must have two projections, has %d", j,
+                           j - 1, pv.np);
+        inp.x1 = pv.pd[1].y;
+      } else if (inp.kind == LBK_INPUT_PLAIN || inp.kind == LBK_INPUT_RMSNORM) {
+        if (pv.np != 1)
+          return set_error(LBK_ERR_ARG, "link %d reads the output of link %d, which must have one projection, has %d",
+                           j, j - 1, pv.np);
+      } else {
+        return set_error(LBK_ERR_ARG, "link %d: input kind %d cannot follow a link (plain, RMSNorm or SiLU * up)", j,
+                         inp.kind);
+      }
+      for (int q = 0; q < pv.np; ++q)
+        if (pv.pd[q].N != c.K)
+          return set_error(LBK_ERR_ARG, "link %d: in_features %lld != out_features %lld of link %d", j,
+                           (long long)c.K, (long long)pv.pd[q].N, j - 1);
+      c.x = pv.pd[0].y;
+    }
+    const int rc = prepare_group(c.pd, c.np, 1, c.K, c.x, LBK_F32, &inp, LBK_F32, c.in, c.pl);
+    if (rc != LBK_OK) {
+      char msg[sizeof(g_last_error)];
+      snprintf(msg, sizeof(msg), "%s", g_last_error);
+      return set_error(rc, "link %d: %s", j, msg);
+    }
+  }
+  fused = n >= 2 && !cl[0].pl.det;
+  for (int j = 0; j < n && fused; ++j) {
+    const ChainLinkDesc& c = cl[j];
+    fused = c.pl.mfma && c.pl.mt == 1 && c.pl.chunk == 0 && c.pl.ks == 1 &&
+            chain_tsize(c.pd, c.np) + kSsqSlots <= kChainRegion;
+    if (!fused || j == 0) continue;
+    // joined to the link before: 16-byte loads of g (and the RMSNorm
+    // weight) by 8-column chunks, V read from its tiled copy, the link
+    // before's steps within the kernel's bound, its staged t and this
+    // link's A operand within LDS
+    fused = c.K % 8 == 0 && (c.in.kind != LBK_INPUT_RMSNORM || aligned16(c.in.nw));
+    for (int q = 0; q < c.np && fused; ++q)
+      for (int b = 0; b < c.pd[q].nb; ++b)
+        fused = fused && aligned16(c.pd[q].br[b].v2) && c.pd[q].br[b].v_sign_tiled;
+    const ChainLinkDesc& pv = cl[j - 1];
+    int64_t chunks = 0;
+    for (int q = 0; q < pv.np && fused; ++q) {
+      fused = proj_steps(pv.pd[q]) <= kChainMaxSteps;
+      for (int b = 0; b < pv.pd[q].nb; ++b) chunks += 16 * ceil_div(ceil_div(pv.pd[q].br[b].rank, 32), 4);
+    }
+    int nseg = 0;
+    for (int q = 0; q < c.np; ++q) nseg += c.pd[q].nb;
+    const int w = chain_waves(pv.pd[0].N);
+    fused = fused && nseg <= w && size_t(chunks + int64_t(nseg) * 2 * w) * 48 <= 64 * 1024;
+  }
+  return LBK_OK;
+}
+
+size_t chain_ws_bytes(const ChainLinkDesc* cl, int n, bool fused) {
+  size_t ws = fused ? kGemmOffset : 0;
+  for (int j = 0; j < n; ++j) ws = std::max(ws, cl[j].pl.ws_min);
+  return ws;
+}
+
+int run_chain(ChainLinkDesc* cl, int n, bool fused, void* workspace, size_t workspace_bytes, void* stream) {
+  const size_t need = chain_ws_bytes(cl, n, fused);
+  if (!workspace || workspace_bytes < need)
+    return set_error(LBK_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!fused) {
+    for (int j = 0; j < n; ++j) {
+      const ChainLinkDesc& c = cl[j];
+      const int rc = run_group(c.pd, c.np, 1, c.K, c.x, LBK_F32, c.in, LBK_F32, c.pl, workspace, workspace_bytes,
+                               stream);
+      if (rc != LBK_OK) return rc;
+    }
+    return LBK_OK;
+  }
+  float* regions = reinterpret_cast<float*>(static_cast<char*>(workspace) + kChainOffset);
+  auto region = [&](int i) { return regions + size_t(i) * kChainRegion; };
+  auto target = [&](int j) { return j == n - 1 ? region(kChainLast) : region(j); };  // region holding link j's t
+  // link 0's latent stage
+  {
+    const ChainLinkDesc& c = cl[0];
+    MfmaParams p;
+    int tiles = 0;
+    int rc = build_mfma_params(c.pd, c.np, c.pl, 1, c.K, c.x, c.in, workspace, p, tiles);
+    if (rc != LBK_OK) return rc;
+    p.tdst = target(0);
+    p.clr = region(kChainLast);
+    p.nclr = kChainRegion;
+    dispatch_latent<float>(p, c.pl, dim3(unsigned(c.pl.nrb * c.pl.nkc), 1u), s);
+    rc = check_launch("latent_mfma_kernel");
+    if (rc != LBK_OK) return rc;
+  }
+  // link j's expand joined to link j + 1's latent stage
+  for (int j = 0; j + 1 < n; ++j) {
+    const ChainLinkDesc& a = cl[j];
+    const ChainLinkDesc& b = cl[j + 1];
+    MfmaParams pe, pb;
+    int tiles = 0;
+    int rc = build_mfma_params(a.pd, a.np, a.pl, 1, a.K, a.x, a.in, workspace, pe, tiles);
+    if (rc != LBK_OK) return rc;
+    rc = build_mfma_params(b.pd, b.np, b.pl, 1, b.K, b.x, b.in, workspace, pb, tiles);
+    if (rc != LBK_OK) return rc;
+    ChainParams cp;
+    memset(&cp, 0, sizeof(cp));
+    cp.tsrc = target(j);
+    cp.tdst = target(j + 1);
+    cp.nw = pb.nw;
+    cp.clr = j > 0 ? region(j - 1) : nullptr;
+    cp.nclr = j > 0 ? int(chain_tsize(cl[j - 1].pd, cl[j - 1].np)) + kSsqSlots : 0;
+    cp.tsize_e = pe.tsize;
+    // link 0's latent kernel applied 1/rms itself unless it deferred it; a
+    // joined kernel always defers it
+    cp.late = j > 0 ? (a.in.kind == LBK_INPUT_RMSNORM ? 1 : 0) : pe.late_rs;
+    cp.Ke = pe.K;
+    cp.N = pe.proj[0].N;
+    cp.eps = pe.eps;
+    cp.nseg = pb.nseg;
+    cp.Kl = pb.K;
+    cp.KWl = pb.KW;
+    cp.xmode = b.in.kind;
+    cp.tsize_l = pb.tsize;
+    for (int q = 0; q < a.np && q < 2; ++q) {
+      const ExpProj& P = pe.proj[q];
+      ChainProj& C = cp.proj[q];
+      for (int br = 0; br < 2; ++br) {
+        C.U[br] = P.U[br];
+        C.h[br] = P.h[br];
+        C.RW[br] = P.RW[br];
+        C.steps[br] = P.RWp[br] / 4;
+        C.tbase[br] = P.tbase[br];
+      }
+      C.bias = P.bias;
+      C.res = P.res;
+      C.y = static_cast<float*>(P.y);
+      C.nb = P.nb;
+    }
+    for (int i = 0; i < pb.nseg; ++i)
+      cp.seg[i] = ChainSeg{pb.seg[i].Vt, pb.seg[i].l, pb.seg[i].g, pb.seg[i].R, pb.seg[i].tbase};
+    const int nt = b.in.kind == LBK_INPUT_SILU_MUL ? 2 : 1;
+    int64_t steps = 0, chunks = 0;
+    for (int q = 0; q < nt; ++q) {
+      steps = std::max(steps, proj_steps(a.pd[q]));
+      for (int br = 0; br < a.pd[q].nb; ++br) chunks += 16 * ceil_div(ceil_div(a.pd[q].br[br].rank, 32), 4);
+    }
+    const int w = chain_waves(a.pd[0].N);
+    const size_t lds = size_t(chunks + int64_t(cp.nseg) * 2 * w) * 48;
+    const unsigned blocks = unsigned(ceil_div(a.pd[0].N, int64_t(16 * w)));
+    dispatch_chain(cp, steps <= 4 ? 4 : steps <= 8 ? 8 : 16, w, nt, blocks, lds, s);
+    rc = check_launch("chain_mfma_kernel");
+    if (rc != LBK_OK) return rc;
+  }
+  // link n - 1's expand stage
+  {
+    const ChainLinkDesc& c = cl[n - 1];
+    MfmaParams p;
+    int tiles = 0;
+    int rc = build_mfma_params(c.pd, c.np, c.pl, 1, c.K, c.x, c.in, workspace, p, tiles);
+    if (rc != LBK_OK) return rc;
+    p.late_rs = c.in.kind == LBK_INPUT_RMSNORM ? 1 : 0;  // the joined kernel left 1/rms out
+    p.tsrc = target(n - 1);
+    p.clr = region(n - 2);
+    p.nclr = int(chain_tsize(cl[n - 2].pd, cl[n - 2].np)) + kSsqSlots;
+    dispatch_expand<float>(p, c.pl, dim3(unsigned(tiles), 1u, 1u), s);
+    return check_launch("expand_mfma_kernel");
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Allocation-free forward: the workspace is a file-scope device array.
 // Each GPU the library runs on holds its own copy of `scratch` until the
 // process ends.  In host code `scratch` names a host-side stand-in, not the
@@ -4059,6 +4719,50 @@ int lbk_group_forward_noalloc(const lbk_projection* projs, int n_proj, int64_t M
   rc = run_group(pd, n_proj, M, K, x, x_dtype, in, y_dtype, pl, ws, kScratchBytes, stream);
   if (rc == LBK_ERR_HIP) scratch_dirty();
   return rc;
+}
+
+size_t lbk_chain_workspace_bytes(const lbk_chain_link* links, int n_links) {
+  g_last_error[0] = '\0';
+  if (!links || n_links < 1 || n_links > kMaxChainLinks) {
+    set_error(LBK_ERR_ARG, "n_links must be in [1, %d] with a non-NULL array, got %d", kMaxChainLinks, n_links);
+    return 0;
+  }
+  // the decode-path workspace of each link, and the chains' regions
+  size_t ws = kGemmOffset;
+  for (int j = 0; j < n_links; ++j) {
+    const lbk_chain_link& lk = links[j];
+    if (!lk.projs || lk.n_proj < 1 || lk.n_proj > kMaxProj) {
+      set_error(LBK_ERR_ARG, "link %d: n_proj must be in [1, %d] with a non-NULL array, got %d", j, kMaxProj,
+                lk.n_proj);
+      return 0;
+    }
+    ProjDesc pd[kMaxProj];
+    for (int q = 0; q < lk.n_proj; ++q)
+      pd[q] = ProjDesc{lk.projs[q].branches, lk.projs[q].n_branches, lk.projs[q].out_features, lk.projs[q].bias,
+                       lk.projs[q].y, lk.projs[q].residual};
+    if (validate_group(pd, lk.n_proj, 1, lk.in_features) != LBK_OK) return 0;
+    ws = std::max(ws, query_workspace(pd, lk.n_proj, 1, lk.in_features));
+  }
+  return ws;
+}
+
+int lbk_chain_forward(const lbk_chain_link* links, int n_links, const void* x, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  g_last_error[0] = '\0';
+  ChainLinkDesc cl[kMaxChainLinks];
+  bool fused = false;
+  const int rc = prepare_chain(links, n_links, x, cl, fused);
+  if (rc != LBK_OK) return rc;
+  return run_chain(cl, n_links, fused, workspace, workspace_bytes, stream);
+}
+
+int lbk_chain_fused(const lbk_chain_link* links, int n_links, const void* x) {
+  g_last_error[0] = '\0';
+  ChainLinkDesc cl[kMaxChainLinks];
+  bool fused = false;
+  const int rc = prepare_chain(links, n_links, x, cl, fused);
+  if (rc != LBK_OK) return rc;
+  return fused ? 1 : 0;
 }
 
 int lbk_group_forward(const lbk_projection* projs, int n_proj, int64_t M, int64_t K, const void* x, int x_dtype,

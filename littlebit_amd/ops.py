@@ -12,6 +12,9 @@
   same input (q/k/v, gate/up) in the launches of one, through
   ``lbk_group_forward`` -- the GPU form of the reference decode step's
   batched q/k/v and gate/up stages (patch:1697-1723, 1777-1798).
+* :class:`LittleBitChain` runs calls that each read the one before's outputs
+  (o, gate/up, down, next q/k/v) at one row in one launch per link boundary,
+  through ``lbk_chain_forward`` (the reference's one-call layer, patch:1627-1833).
 
 Everything here requires CUDA (HIP) tensors; there is no CPU path.
 """
@@ -31,6 +34,8 @@ __all__ = [
     "LittleBitBranch",
     "LittleBitProjection",
     "LittleBitProjectionGroup",
+    "ChainLink",
+    "LittleBitChain",
     "littlebit_linear",
     "littlebit_forward",
     "workspace_for",
@@ -441,6 +446,155 @@ class LittleBitProjectionGroup:
                                       _DTYPE_CODES[odt], ws.data_ptr(), ws.numel(), stream)
         _call(rc, "lbk_group_forward_ex", x2.device, stream)
         return list(outs)
+
+    __call__ = forward
+
+
+class ChainLink:
+    """One call of a :class:`LittleBitChain`: projections that read one input
+    (a :class:`LittleBitProjection`, a :class:`LittleBitProjectionGroup` or a
+    list of projections), their fp32 output tensors [1, N] and optional fp32
+    residuals (each may be its output tensor itself: x += projection(...)).
+
+    How the link reads its input -- for the first link the chain's x, for
+    the others the outputs of the link before:
+      ``rms_weight``  RMSNorm(input) * rms_weight (the link before has one projection);
+      ``silu_mul``    SiLU(gate) * up of the link before's two projections
+                      (the first link gets x_up at :meth:`LittleBitChain.forward`);
+      neither         the input itself (the link before has one projection).
+    """
+
+    def __init__(self, projections, outs: Sequence[torch.Tensor], *,
+                 residuals: Optional[Sequence[Optional[torch.Tensor]]] = None,
+                 rms_weight: Optional[torch.Tensor] = None, rms_eps: float = 1e-6, silu_mul: bool = False):
+        if isinstance(projections, LittleBitProjection):
+            projections = [projections]
+        elif isinstance(projections, LittleBitProjectionGroup):
+            projections = projections.projections
+        self.projections = list(projections)
+        _check(1 <= len(self.projections) <= _lib.LBK_MAX_GROUP,
+               f"a link has 1 to {_lib.LBK_MAX_GROUP} projections, got {len(self.projections)}")
+        _check(not (rms_weight is not None and silu_mul), "rms_weight and silu_mul exclude each other")
+        self.in_features = self.projections[0].in_features
+        for i, p in enumerate(self.projections):
+            _check(p.in_features == self.in_features, f"projection {i}: in_features differs within the link")
+        _check(len(outs) == len(self.projections), "one output per projection")
+        for o, p in zip(outs, self.projections):
+            _require_cuda(o, "out")
+            _check(o.dtype == torch.float32 and o.is_contiguous() and o.numel() == p.out_features,
+                   "an output must be a contiguous float32 tensor with out_features elements (one row)")
+        self.outs = list(outs)
+        self.residuals = list(residuals) if residuals is not None else [None] * len(self.projections)
+        _check(len(self.residuals) == len(self.projections), "one residual (or None) per projection")
+        for r, p in zip(self.residuals, self.projections):
+            if r is not None:
+                _require_cuda(r, "residual")
+                _check(r.dtype == torch.float32 and r.numel() == p.out_features,
+                       "a residual must be float32 with out_features elements")
+        if rms_weight is not None:
+            _require_cuda(rms_weight, "rms_weight")
+            _check(rms_weight.dtype == torch.float32 and rms_weight.numel() == self.in_features,
+                   "rms_weight must be float32 with in_features elements")
+        self.rms_weight = rms_weight
+        self.rms_eps = float(rms_eps)
+        self.silu_mul = bool(silu_mul)
+
+
+class LittleBitChain:
+    """Calls in sequence at one row, each reading the outputs of the one
+    before (``lbk_chain_forward``): o, gate/up, down and the next layer's
+    q/k/v of a decode step.  Same results as running the links one by one
+    with :meth:`LittleBitProjectionGroup.forward`; n links take n + 1
+    launches instead of 2 n (the kernel between two links expands the first
+    link's rows and adds their part of the next link's latent vector).  The
+    reference runs a decoder layer's projections in one call
+    (patches/littlebit_cpu_optimized.cpp:1627-1833).  The output and residual
+    tensors are fixed when the chain is made, so it can be captured in a HIP
+    graph."""
+
+    def __init__(self, links: Sequence[ChainLink]):
+        _check(1 <= len(links) <= _lib.LBK_MAX_CHAIN, f"a chain has 1 to {_lib.LBK_MAX_CHAIN} links")
+        self.links = list(links)
+        self.device = self.links[0].projections[0].device
+        self._keep = []
+        arr = (_lib.LbkChainLink * len(self.links))()
+        for j, lk in enumerate(self.links):
+            projs = (_lib.LbkProjection * len(lk.projections))()
+            for i, p in enumerate(lk.projections):
+                _check(p.device == self.device, "all projections of a chain must be on one device")
+                projs[i].branches = ctypes.cast(p._arr, ctypes.POINTER(_lib.LbkBranch))
+                projs[i].n_branches = len(p.branches)
+                projs[i].out_features = p.out_features
+                projs[i].bias = p.bias.data_ptr() if p.bias is not None else None
+                projs[i].y = lk.outs[i].data_ptr()
+                projs[i].residual = None if lk.residuals[i] is None else lk.residuals[i].data_ptr()
+            if lk.rms_weight is not None:
+                inp = _lib.LbkInput(_lib.LBK_INPUT_RMSNORM, lk.rms_weight.data_ptr(), lk.rms_eps, None)
+            elif lk.silu_mul:
+                inp = _lib.LbkInput(_lib.LBK_INPUT_SILU_MUL, None, 0.0, None)
+            else:
+                inp = _lib.LbkInput(_lib.LBK_INPUT_PLAIN, None, 0.0, None)
+            self._keep += [projs, inp, lk.projections]
+            arr[j].projs = ctypes.cast(projs, ctypes.POINTER(_lib.LbkProjection))
+            arr[j].n_proj = len(lk.projections)
+            arr[j].in_features = lk.in_features
+            arr[j].input = ctypes.pointer(inp)
+        self._arr = arr
+        self._inp0 = self._keep[1]
+        lib = _lib.load()
+        n = lib.lbk_chain_workspace_bytes(arr, len(self.links))
+        if n == 0:
+            _lib.check(_lib.LBK_ERR_ARG, "lbk_chain_workspace_bytes")
+        self._ws_bytes = int(n)
+
+    def fused(self, x: Optional[torch.Tensor] = None, attn: Optional[AttentionPartials] = None) -> bool:
+        """Whether the links run joined (n + 1 launches) for this input."""
+        ptr = self._set_input(x, attn, None)
+        rc = _lib.load().lbk_chain_fused(self._arr, len(self.links), ptr)
+        if rc < 0:
+            _lib.check(rc, "lbk_chain_fused")
+        return rc == 1
+
+    def _set_input(self, x, attn, x_up):
+        lk = self.links[0]
+        inp = self._inp0
+        if attn is not None:
+            _check(x is None and x_up is None and lk.rms_weight is None and not lk.silu_mul,
+                   "attn replaces x and the first link's other input fusions")
+            part = attn.partials
+            _require_cuda(part, "attn.partials")
+            _check(part.dtype == torch.float32 and part.is_contiguous() and part.device == self.device,
+                   "attn.partials must be a contiguous float32 tensor on the chain's device")
+            inp.kind = _lib.LBK_INPUT_ATTN_MERGE
+            inp.head_dim = int(attn.head_dim)
+            inp.max_seq = int(attn.max_seq)
+            inp.pos_device = None if attn.pos is None else attn.pos.data_ptr()
+            inp.pos = int(attn.pos_host)
+            return part.data_ptr()
+        _check(isinstance(x, torch.Tensor) and x.is_cuda and x.device == self.device, "x must be a GPU tensor on the chain's device")
+        _check(x.dtype == torch.float32 and x.is_contiguous() and x.numel() == lk.in_features,
+               "x must be a contiguous float32 tensor with the first link's in_features elements (one row)")
+        if lk.rms_weight is not None:
+            inp.kind = _lib.LBK_INPUT_RMSNORM
+        elif lk.silu_mul:
+            _check(isinstance(x_up, torch.Tensor) and x_up.is_cuda and x_up.dtype == torch.float32
+                   and x_up.is_contiguous() and x_up.numel() == x.numel(), "the first link's SiLU * up needs x_up like x")
+            inp.kind = _lib.LBK_INPUT_SILU_MUL
+            inp.x1 = x_up.data_ptr()
+        else:
+            inp.kind = _lib.LBK_INPUT_PLAIN
+        return x.data_ptr()
+
+    def forward(self, x: Optional[torch.Tensor] = None, *, attn: Optional[AttentionPartials] = None,
+                x_up: Optional[torch.Tensor] = None) -> None:
+        """Run the chain on x [1, K] fp32 (or the attention partials ``attn``);
+        the results are in the links' output tensors."""
+        ptr = self._set_input(x, attn, x_up)
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        ws = workspace_for(self.device, stream, self._ws_bytes)
+        rc = lib.lbk_chain_forward(self._arr, len(self.links), ptr, ws.data_ptr(), ws.numel(), stream)
+        _call(rc, "lbk_chain_forward", self.device, stream)
 
     __call__ = forward
 
