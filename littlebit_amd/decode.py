@@ -151,6 +151,7 @@ class LittleBitDecoder:
             nbytes = _lib.load().lbk_attention_partial_bytes(c.num_attention_heads, self.max_seq_len, c.head_dim)
             self._attn_part = torch.empty(max(int(nbytes) // 4, 1), dtype=torch.float32, device=dev)
         self._batch_part = None  # partials of the batched attention, grown as needed
+        self._chains = None  # one-token steps: each layer's o .. next q/k/v as one LittleBitChain
 
     def reset(self):
         """Forget the cached positions (the reference's _LBModelUnit.reset)."""
@@ -281,8 +282,10 @@ class LittleBitDecoder:
             return rms_norm(x, self.final_norm, eps) if final_norm else x
         # the norms, SiLU * up and the residual adds run inside the projection
         # calls; x (a private copy) is updated in place by o and down
-        x = x.to(torch.float32).clone()
         merge = x.shape[0] == 1 and tree_mask is None and self._hip_attn
+        if merge:
+            return self._forward_one_chained(x, start, pos_t, final_norm)
+        x = x.to(torch.float32).clone()
         if tree_mask is not None and self._hip_attn:
             # the batched attention kernel reads the mask as bytes: convert it
             # once here rather than in every layer (a copy launch per layer)
@@ -297,6 +300,47 @@ class LittleBitDecoder:
             g, u = L["gate_up"].forward(x, rms_weight=L["ln2"], rms_eps=eps)
             L["down"].forward(g, out=x, residual=x, x_up=u)
         return rms_norm(x, self.final_norm, eps) if final_norm else x
+
+    def _chain_buffers(self):
+        """Persistent one-row buffers and, per layer, the chain o -> gate/up ->
+        down -> next layer's q/k/v (the last layer's ends at down), made once:
+        the chains are bound to these buffers."""
+        if self._chains is not None:
+            return
+        from .ops import ChainLink, LittleBitChain
+        c, dev = self.config, self.device
+        z = lambda n: torch.zeros((1, n), dtype=torch.float32, device=dev)  # noqa: E731
+        L0 = self.layers[0]
+        self._cx = z(c.hidden_size)
+        self._cq, self._ck, self._cv = (z(p.out_features) for p in L0["qkv"].projections)
+        self._cg, self._cu = (z(p.out_features) for p in L0["gate_up"].projections)
+        eps = c.rms_norm_eps
+        chains = []
+        for li, L in enumerate(self.layers):
+            links = [ChainLink(L["o"], [self._cx], residuals=[self._cx]),
+                     ChainLink(L["gate_up"], [self._cg, self._cu], rms_weight=L["ln2"], rms_eps=eps),
+                     ChainLink(L["down"], [self._cx], residuals=[self._cx], silu_mul=True)]
+            if li + 1 < len(self.layers):
+                nx = self.layers[li + 1]
+                links.append(ChainLink(nx["qkv"], [self._cq, self._ck, self._cv], rms_weight=nx["ln1"], rms_eps=eps))
+            chains.append(LittleBitChain(links))
+        self._chains = chains
+
+    def _forward_one_chained(self, x: torch.Tensor, start: int, pos_t: Optional[torch.Tensor],
+                             final_norm: bool) -> torch.Tensor:
+        """One token: layer 0's q/k/v, then per layer the attention (stopped at
+        its partials) and one chain from o through the next layer's q/k/v,
+        which runs the layer's calls in one launch per call boundary
+        (lbk_chain_forward; the reference's full_forward runs a layer as one
+        call, patches/littlebit_cpu_optimized.cpp:1627-1833)."""
+        self._chain_buffers()
+        eps = self.config.rms_norm_eps
+        self._cx.copy_(x.reshape(1, -1))
+        L0 = self.layers[0]
+        L0["qkv"].forward(self._cx, outs=[self._cq, self._ck, self._cv], rms_weight=L0["ln1"], rms_eps=eps)
+        for li, chain in enumerate(self._chains):
+            chain.forward(attn=self._attention_partials(li, self._cq, self._ck, self._cv, start, pos_t))
+        return rms_norm(self._cx, self.final_norm, eps) if final_norm else self._cx.clone()
 
     def forward_batch(self, token_ids: Sequence[int], embed_tokens: torch.Tensor,
                       tree_mask: Optional[torch.Tensor] = None, final_norm: bool = True) -> torch.Tensor:
