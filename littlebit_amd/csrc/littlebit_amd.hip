@@ -1764,11 +1764,13 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
   const bool gin = wave < nseg && ac < NCH && ak < cp.Kl;  // K % 8 == 0: wholly inside or past K
   Raw8<float> g8;
   g8.load(G.g + (gin ? ak : 0));
-  // the V words of the wave's first TPW tiles: one round trip for them all
+  // the V words of the wave's first TPW tiles (those it has): one round trip
+  // for them all
   uint32_t vw[TPW][NVW];
   float lv[TPW];
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) load_vw(i, vw[i], lv[i]);
+  for (int i = 0; i < TPW; ++i)
+    if (wi + i * nws < ntile) load_vw(i, vw[i], lv[i]);
   const float nwv = cp.xmode == LBK_INPUT_RMSNORM ? cp.nw[nc] : 1.f;
   // (5) the region this launch clears
   {
@@ -1893,10 +1895,16 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
 
   // (9) the wave's latent tiles in batches of TPW: NVW MFMAs each over the
   // k-chunk, then one fp32 atomic per latent row
+  // the segment's A operand: the same NVW fragments for every tile
+  bf16x8 aop[NVW];
+#pragma unroll
+  for (int kk = 0; kk < NVW; ++kk)
+    aop[kk] = __builtin_bit_cast(bf16x8, lds_a[(size_t(ws) * NCH + 4 * kk + grp) * L::ROWS + lrow]);
   for (int k0 = 0; k0 * nws + wi < ntile; k0 += TPW) {
     if (k0 > 0) {
 #pragma unroll
-      for (int i = 0; i < TPW; ++i) load_vw(k0 + i, vw[i], lv[i]);
+      for (int i = 0; i < TPW; ++i)
+        if (wi + (k0 + i) * nws < ntile) load_vw(k0 + i, vw[i], lv[i]);
     }
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -1906,8 +1914,7 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
 #pragma unroll
       for (int kk = 0; kk < NVW; ++kk) {
         const bf16x8 bop = signs_to_bf16x8(vw[i][kk], grp, kmask, kone);
-        const bf16x8 aop = __builtin_bit_cast(bf16x8, lds_a[(size_t(ws) * NCH + 4 * kk + grp) * L::ROWS + lrow]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[kk], bop, acc, 0, 0, 0);
       }
       const float sum = acc[0] + __shfl_xor(acc[0], 32);
       const int r = 16 * t + col;
