@@ -3,19 +3,25 @@
 Workload: the Llama-2-7B-shaped 0.1-BPW draft decode
 step -- the 7 projections of each of 32 decoder layers at batch 1 (q, k, v, o
 4096->4096 rank 205; gate, up 4096->11008 rank 298; down 11008->4096 rank
-298), fp32 activations, random packed signs and |N(0,1)|+0.05 scales.  One
-step = the 224 forwards in decode order, captured as one HIP graph; per layer
-four calls: q/k/v as one group call (they read the same input), o, gate/up as
-one group call, down -- two kernel launches per call.
+298), fp32 activations, random packed signs and |N(0,1)|+0.05 scales, with
+the decode step's data flow (ChainStep): q/k/v of RMSNorm(x), o of a fixed
+stand-in for the attention output added to x, gate/up of RMSNorm(x), down of
+SiLU(gate) * up added to x.  One step = the 224 forwards captured as one HIP
+graph; each layer's o, gate/up, down and the next layer's q/k/v run as one
+LittleBitChain (lbk_chain_forward: 5 launches per layer, each kernel between
+two calls expanding one call's rows and adding their part of the next call's
+latent vector).  The same step with each call on its own (8 launches per
+layer) and the previous workload (224 calls with independent inputs) are
+reported beside it.
 
 value = algorithmic bytes of a step / time of a step, with the weights cold:
 the step rotates over enough weight replicas that the working set exceeds
 the 256 MB Infinity Cache.  The warm figure (one replica) is reported too.
 
-roofline = the call kind with the longest duration, one call = its two
-kernels (latent + expand) and the gap between them, timed with HIP events
-around a graph of 32 back-to-back calls of that kind; bytes per call from
-sign words + scales + x read once + y written once, summed over the call's projections.  cpu_baseline = the reference AVX2 kernel littlebit_linear
+roofline = the dominant unit of the step, one layer's chain (its 5 kernels,
+7 projections), timed with HIP events around the step's graphs (32 layer
+chains each); bytes from sign words + scales + x read once + y written once
+per projection.  cpu_baseline = the reference AVX2 kernel littlebit_linear
 (oracle/_ref, built from the reference source) on the host cores, over a
 bounded number of whole steps.
 
@@ -45,6 +51,9 @@ HBM_PEAK_GBS = 8000.0
 MEASURED_TRAFFIC = {"qkv": 1_229_984, "o": 616_288, "gate/up": 1_811_040, "down": 1_128_064}
 # the same for the target's calls at M = 8 (profiles/littlebit_verify_m8_target.md)
 MEASURED_TRAFFIC_M8 = {"qkv": 11_636_122, "o": 5_105_971, "gate/up": 17_666_765, "down": 9_626_419}
+# the same for one layer's chain (latent_mfma_kernel + 3 chain_mfma_kernel +
+# expand_mfma_kernel) of the chained draft step (profiles/littlebit_decode_chain.md)
+MEASURED_TRAFFIC_CHAIN = 4_729_994
 MALL_BYTES = 256 << 20
 
 
@@ -181,7 +190,8 @@ class ChainStep:
                     nx = self.layers[li + 1]
                     links.append(ChainLink(nx["qkv"], [self.q, self.k, self.v], rms_weight=nx["ln1"]))
                 self.chains.append(LittleBitChain(links))
-            assert all(c.fused(self.a) for c in self.chains), "the draft step's chains run joined"
+        # whether every chain runs joined (not in deterministic mode)
+        self.all_joined = joined and all(c.fused(self.a) for c in self.chains)
 
     def run(self):
         L0 = self.layers[0]
@@ -199,11 +209,11 @@ class ChainStep:
                 nx["qkv"].forward(self.x, outs=[self.q, self.k, self.v], rms_weight=nx["ln1"])
 
 
-def chain_step_bench(gen, dev, stream, layers, steps, warmup):
+def chain_step_bench(gen, dev, stream, layers, steps, warmup, forms=(True, False)):
     """The decode step's 224 projections with their data flow, joined into
     chains and one by one, cold (replicas rotated) and warm."""
     out = {}
-    for joined in (True, False):
+    for joined in forms:
         first = ChainStep(gen, dev, layers, joined)
         replicas = max(2, math.ceil(2 * MALL_BYTES / first.weight_bytes))
         reps = [first] + [ChainStep(gen, dev, layers, joined) for _ in range(replicas - 1)]
@@ -778,7 +788,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill measurement")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-2/3 whole-model decode measurement")
     ap.add_argument("--only", choices=["qkv", "o", "gate_up", "down", "prefill", "decode", "draft", "verify", "copy",
-                                       "lm_head", "small", "handoff", "issue", "chain"], default=None,
+                                       "lm_head", "small", "handoff", "issue", "chain", "chain_joined"], default=None,
                     help="profiling aid: replay only this call kind (32 per graph) and print its timing")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -830,8 +840,9 @@ def main():
     if args.only in ("decode", "draft"):
         print(json.dumps(decode_bench(dev, target=args.only == "decode")))
         return
-    if args.only == "chain":
-        print(json.dumps(chain_step_bench(gen, dev, stream, args.layers, args.steps, args.warmup)))
+    if args.only in ("chain", "chain_joined"):
+        forms = (True,) if args.only == "chain_joined" else (True, False)
+        print(json.dumps(chain_step_bench(gen, dev, stream, args.layers, args.steps, args.warmup, forms)))
         return
     if args.only == "verify":
         print(json.dumps(verify_linears_bench(gen, dev, stream, args.layers, steps=args.steps, warmup=args.warmup)))
@@ -842,49 +853,54 @@ def main():
         print(json.dumps({"only": args.only, "projections": list(names), "us_per_call_in_graph": round(us, 3),
                           "bytes_per_call": call.bytes, "gbs": round(call.bytes / us / 1e3, 2)}))
         return
-    first = DraftStep(gen, dev, args.layers)
+    first = ChainStep(gen, dev, args.layers, joined=True)
+    assert first.all_joined, "the chained draft step runs its chains joined"
     step_bytes, weight_bytes = first.bytes, first.weight_bytes
     replicas = max(2, math.ceil(2 * MALL_BYTES / weight_bytes))
-    steps_list = [first] + [DraftStep(gen, dev, args.layers) for _ in range(replicas - 1)]
+    steps_list = [first] + [ChainStep(gen, dev, args.layers, joined=True) for _ in range(replicas - 1)]
     graphs = [capture(s.run, stream) for s in steps_list]
     ms_cold = time_graphs(graphs, args.steps, args.warmup, stream)
     ms_warm = time_graphs(graphs[:1], args.steps, args.warmup, stream)
     del graphs, steps_list, first
-    # the same step in deterministic mode (fixed-order split-K sums by each row-block's last block)
-    import littlebit_amd as lb
-    with lb.deterministic(True):
-        det_steps = [DraftStep(gen, dev, args.layers) for _ in range(replicas)]
-        graphs = [capture(s.run, stream) for s in det_steps]
-        ms_det = time_graphs(graphs, args.steps, args.warmup, stream)
-    del graphs, det_steps
-    # the same step with every projection launched on its own (no groups)
-    single = [DraftStep(gen, dev, args.layers, grouped=False) for _ in range(replicas)]
-    graphs = [capture(s.run, stream) for s in single]
-    ms_single = time_graphs(graphs, args.steps, args.warmup, stream)
-    del graphs, single
 
-    # per call kind: duration in a graph of back-to-back calls of that kind
+    def step_ms(make, det=False):
+        import littlebit_amd as lb
+        with lb.deterministic(det):
+            reps = [make() for _ in range(replicas)]
+            gs = [capture(r.run, stream) for r in reps]
+            ms = time_graphs(gs, args.steps, args.warmup, stream)
+        del gs, reps
+        return ms
+    # the same step with each call on its own (two launches per call)
+    ms_one = step_ms(lambda: ChainStep(gen, dev, args.layers, joined=False))
+    # in deterministic mode the chains run as separate calls, with fixed-order split-K sums
+    ms_det = step_ms(lambda: ChainStep(gen, dev, args.layers, joined=True), det=True)
+    # the previous workload: 224 calls with independent inputs, grouped, and every projection alone
+    ms_indep = step_ms(lambda: DraftStep(gen, dev, args.layers))
+    ms_single = step_ms(lambda: DraftStep(gen, dev, args.layers, grouped=False))
+
+    # per call kind (each call alone): duration in a graph of back-to-back calls of that kind
     cls_stats = {}
     for kind, names in LAYER_CALLS:
         call, us = call_duration_us(gen, dev, names, stream)
         cls_stats[kind] = {"projections": "+".join(names), "us_per_call": round(us, 3), "bytes": call.bytes,
                            "gbs": call.bytes / us / 1e3}
-    # the dominant call kind: the longest call (each kind runs once per layer),
-    # and among kinds within 2 % of it (a tie within run-to-run noise) the one
-    # that moves the most bytes, so the choice does not flip between runs
-    longest = max(v["us_per_call"] for v in cls_stats.values())
-    dom = max((c for c in cls_stats if cls_stats[c]["us_per_call"] >= 0.98 * longest),
-              key=lambda c: cls_stats[c]["bytes"])
-    d = cls_stats[dom]
     ceiling = copy_ceiling(dev, stream)
     floor_us = launch_floor_us(dev, stream)
-    roofline = {"bound": "hbm", "achieved": round(d["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["gbs"] / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC.get(dom),
-                "traffic_source": "not measured in this run: calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE of the "
-                                  "same call kind, profiles/littlebit_decode_calls.md",
-                "copy_ceiling_gbs": ceiling["gbs"], "frac_of_copy_ceiling": round(d["gbs"] / ceiling["gbs"], 5),
-                "kernel": f"LittleBitLinear {dom} call ({d['projections']}): latent_mfma_kernel + expand_mfma_kernel",
-                "bytes_per_launch": d["bytes"], "us_per_launch": d["us_per_call"]}
+    # the dominant unit of the step: one layer's chain (7 projections, 5
+    # kernels: o's latent stage, three joined kernels, q/k/v's expand stage),
+    # the step's HIP-event time per layer
+    layer_bytes = step_bytes / args.layers
+    layer_us = ms_cold * 1000.0 / args.layers
+    layer_gbs = layer_bytes / layer_us / 1e3
+    roofline = {"bound": "hbm", "achieved": round(layer_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(layer_gbs / HBM_PEAK_GBS, 5), "traffic": MEASURED_TRAFFIC_CHAIN,
+                "traffic_source": "not measured in this run: calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE of one "
+                                  "layer's chain kernels, profiles/littlebit_decode_chain.md",
+                "copy_ceiling_gbs": ceiling["gbs"], "frac_of_copy_ceiling": round(layer_gbs / ceiling["gbs"], 5),
+                "kernel": "one layer's LittleBitChain o -> gate/up -> down -> next q/k/v: latent_mfma_kernel + "
+                          "3 x chain_mfma_kernel + expand_mfma_kernel",
+                "bytes_per_launch": round(layer_bytes), "us_per_launch": round(layer_us, 3)}
 
     small = small_configs_bench(gen, dev, stream)
     verify_lin = verify_linears_bench(gen, dev, stream, args.layers)
@@ -906,8 +922,10 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "llama2-7b-draft-0.1bpw-decode-step (224 LittleBitLinear forwards, M=1)",
-                   "launches": f"{2 * len(LAYER_CALLS)} per layer: q/k/v and gate/up as group calls",
+        "config": {"workload": "llama2-7b-draft-0.1bpw-decode-step (224 LittleBitLinear forwards, M=1, the decode "
+                               "step's data flow: RMSNorm, SiLU * up and residual adds fused)",
+                   "launches": "5 per layer: o -> gate/up -> down -> next q/k/v as one LittleBitChain "
+                               "(2 for layer 0's q/k/v)",
                    "layers": args.layers, "hidden": 4096, "intermediate": 11008,
                    "ranks": {"attn": 205, "mlp": 298}, "batch": 1, "activations": "fp32",
                    "bytes_per_step": step_bytes, "weight_bytes_per_step": weight_bytes,
@@ -917,11 +935,18 @@ def main():
         "tok_per_s_linears": round(1000.0 / ms_cold, 2),
         "warm": {"ms_per_step": round(ms_warm, 4), "value": round(step_bytes / (ms_warm * 1e-3) / 1e9, 3),
                  "us_per_layer": round(ms_warm * 1000.0 / args.layers, 3)},
+        "one_by_one": {"ms_per_step": round(ms_one, 4), "value": round(step_bytes / (ms_one * 1e-3) / 1e9, 3),
+                       "launches": "8 per layer: the same calls each on its own (q/k/v and gate/up as group "
+                                   "calls), cold"},
+        "independent_calls": {"ms_per_step": round(ms_indep, 4),
+                              "value": round(step_bytes / (ms_indep * 1e-3) / 1e9, 3),
+                              "launches": "8 per layer: 224 calls with independent plain inputs (q/k/v and "
+                                          "gate/up grouped), cold"},
         "ungrouped": {"ms_per_step": round(ms_single, 4), "value": round(step_bytes / (ms_single * 1e-3) / 1e9, 3),
-                      "launches": "14 per layer (each projection alone), cold"},
+                      "launches": "14 per layer (independent calls, each projection alone), cold"},
         "deterministic": {"ms_per_step": round(ms_det, 4), "value": round(step_bytes / (ms_det * 1e-3) / 1e9, 3),
-                          "note": "lbk_set_deterministic(1): split-K partials summed in chunk order, bit-for-bit "
-                                  "repeatable; cold"},
+                          "note": "lbk_set_deterministic(1): the chains run as separate calls, split-K partials "
+                                  "summed in chunk order, bit-for-bit repeatable; cold"},
         "per_class": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in cls_stats.items()},
         "roofline": roofline,
@@ -930,8 +955,9 @@ def main():
                      "launch_floor_us_per_call": round(floor_us, 3),
                      "launch_floor_ms_per_step": round(floor_us * len(LAYER_CALLS) * args.layers / 1000.0, 4),
                      "launch_floor_note": "smallest decode-path call (K = N = 256, rank 8, M = 1): the latent + "
-                                          "expand launches with almost no work, in a graph of 32 calls; a draft "
-                                          f"step is {len(LAYER_CALLS) * args.layers} such calls",
+                                          "expand launches with almost no work, in a graph of 32 calls; a step "
+                                          f"of calls each on its own is {len(LAYER_CALLS) * args.layers} such "
+                                          "calls, the chained step 5/8 as many launches",
                      "stage_handoff": handoff},
         "configs_0_1": small,
         "verify_linears": verify_lin,
