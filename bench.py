@@ -884,7 +884,7 @@ def main():
     for kind, names in LAYER_CALLS:
         call, us = call_duration_us(gen, dev, names, stream)
         cls_stats[kind] = {"projections": "+".join(names), "us_per_call": round(us, 3), "bytes": call.bytes,
-                           "gbs": call.bytes / us / 1e3}
+                           "gbs": call.bytes / us / 1e3, "traffic": MEASURED_TRAFFIC.get(kind)}
     ceiling = copy_ceiling(dev, stream)
     floor_us = launch_floor_us(dev, stream)
     # the dominant unit of the step: one layer's chain (7 projections, 5
