@@ -329,6 +329,26 @@ __device__ __forceinline__ void split8(const float (&a)[8], u32x4& hi, u32x4& lo
   }
 }
 
+// x of lane l plus x of lane l + 32, in lanes 0..31 (lanes 32..63 get 2x;
+// every caller reads the lower half only): MFMA C rows 0..7 (lanes 0..31)
+// and 8..15 (lanes 32..63) hold the hi and lo parts of the same sums.
+// v_permlane32_swap moves the upper half down in one VALU op; a shuffle
+// through ds_bpermute costs an LDS round trip and a wait.
+__device__ __forceinline__ float add_upper32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return x + __uint_as_float(r[1]);
+}
+
+// Sum over each row of 16 lanes, in every lane of the row: four DPP adds
+// (quad swaps 1 and 2, then the half-row and row mirrors).
+__device__ __forceinline__ float row16_sum(float s) {
+  s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xb1, 0xf, 0xf, false));
+  s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4e, 0xf, 0xf, false));
+  s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xf, 0xf, false));
+  s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x140, 0xf, 0xf, false));
+  return s;
+}
+
 // The same for W = 4 or 8 floats, as W / 2 dwords each.
 template <int W>
 __device__ __forceinline__ void split_pairs(const float (&a)[W], uint32_t (&hi)[W / 2], uint32_t (&lo)[W / 2]) {
@@ -910,7 +930,7 @@ __global__ __launch_bounds__(kBlock) void latent_mfma_kernel(MfmaParams p) {
 #pragma unroll
   for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sum[mb][i] = acc[mb][i] + __shfl_xor(acc[mb][i], 32);
+    for (int i = 0; i < 4; ++i) sum[mb][i] = add_upper32(acc[mb][i]);
 
   float* trow = (p.tdst ? p.tdst : p.t2 + size_t(h) * kTHalf) + tb + r;
   if constexpr (DET) {
@@ -1488,8 +1508,7 @@ __global__ __launch_bounds__(WAVES * kWave, WAVES == 8 && MT == 8 && S <= 24 ? 4
   for (int mb = 0; mb < L::MB; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      out[mb][i] = h0v * (acc0[mb][i] + __shfl_xor(acc0[mb][i], 32)) +
-                   h1 * (acc[mb][i] + __shfl_xor(acc[mb][i], 32));
+      out[mb][i] = h0v * add_upper32(acc0[mb][i]) + h1 * add_upper32(acc[mb][i]);
 
   // (6) the other parts of the tile add theirs through LDS
   if (splits > 1) {
@@ -1727,6 +1746,9 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
     bnv[q] = P.bias ? P.bias[nc] : 0.f;
     resv[q] = P.res ? P.res[nc] : 0.f;
   }
+  // link j + 1's RMSNorm weight at k = n, before the V words below (waits
+  // retire in issue order: a load after them would wait for them)
+  const float nwv = cp.xmode == LBK_INPUT_RMSNORM ? cp.nw[nc] : 1.f;
   // (4) link j + 1's latent stage (its segment's fields were read first)
   const int kw0 = c0 / 32;
   const int kw4 = (cp.KWl + 3) >> 2;
@@ -1771,7 +1793,6 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
 #pragma unroll
   for (int i = 0; i < TPW; ++i)
     if (wi + i * nws < ntile) load_vw(i, vw[i], lv[i]);
-  const float nwv = cp.xmode == LBK_INPUT_RMSNORM ? cp.nw[nc] : 1.f;
   // (5) the region this launch clears
   {
     const int nblk = int(gridDim.x), bl = int(blockIdx.x);
@@ -1843,8 +1864,8 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
       acc = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     // C row 0 (lanes 0..15) is hi of the row, C row 8 (lanes 32..47) lo
-    const float s0 = acc0[0] + __shfl_xor(acc0[0], 32);
-    const float s1 = acc[0] + __shfl_xor(acc[0], 32);
+    const float s0 = add_upper32(acc0[0]);
+    const float s1 = add_upper32(acc[0]);
     y[q] = h0v[q] * s0 + h1v[q] * s1 + bnv[q] + resv[q];
   }
   // (7) link j's outputs, and link j + 1's input at k = n
@@ -1861,9 +1882,7 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
   }
   if (cp.xmode == LBK_INPUT_RMSNORM) {
     // the rows' sum of squares: lanes 0..15 of each wave, then the block
-    float q2 = lane < 16 && nvalid ? y[0] * y[0] : 0.f;
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) q2 += __shfl_xor(q2, o);
+    const float q2 = row16_sum(lane < 16 && nvalid ? y[0] * y[0] : 0.f);
     if (lane == 0) ssqw[wave] = q2;
   }
   __syncthreads();
@@ -1916,7 +1935,7 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
         const bf16x8 bop = signs_to_bf16x8(vw[i][kk], grp, kmask, kone);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[kk], bop, acc, 0, 0, 0);
       }
-      const float sum = acc[0] + __shfl_xor(acc[0], 32);
+      const float sum = add_upper32(acc[0]);
       const int r = 16 * t + col;
       if (lane < 16 && r < G.R) unsafeAtomicAdd(cp.tdst + G.tbase + r, lv[i] * sum);
     }
