@@ -247,3 +247,85 @@ def test_chain_invalid_links(gpu):
         LittleBitChain([ChainLink(Ly.p["gate"], [g]), ChainLink(Ly.p["o"], [x])]).forward(
             torch.zeros((1, 256), device=gpu))
     assert "link 1" in L.load().lbk_last_error().decode()
+
+
+def test_chain_eight_links(gpu):
+    """The longest chain (LBK_MAX_CHAIN links): every latent region in use,
+    the last link's region the last one, links of every input kind (plain,
+    RMSNorm, two projections then SiLU * up), two-branch and ragged ranks, a
+    bias and an output that is also its own residual; against the float64
+    oracle and the same links one by one, on two calls in a row (the regions
+    a chain leaves behind must not leak into the next call)."""
+    from littlebit_amd import ChainLink, LittleBitChain, LittleBitProjectionGroup
+    specs = [  # name, K, N, ranks, bias
+        ("a", 512, 640, [40], False), ("b", 640, 512, [24, 56], False), ("c", 512, 768, [64], False),
+        ("d", 768, 384, [33], False), ("g", 384, 1000, [48], False), ("u", 384, 1000, [48], True),
+        ("e", 1000, 384, [30, 70], False), ("f", 384, 512, [20], False), ("h", 512, 256, [36, 12], True)]
+    P, H, B = {}, {}, {}
+    for i, (nm, K, N, ranks, bias) in enumerate(specs):
+        P[nm], H[nm], B[nm] = _proj(9100 + 17 * i, K, N, ranks, gpu, bias=bias)
+    rng = np.random.Generator(np.random.PCG64(9199))
+    w_c = (rng.random(512) + 0.5).astype(np.float32)
+    w_g = (rng.random(384) + 0.5).astype(np.float32)
+    w_h = (rng.random(512) + 0.5).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(gpu)  # noqa: E731
+    tw_c, tw_g, tw_h = t(w_c), t(w_g), t(w_h)
+    nan = lambda n: torch.full((1, n), float("nan"), device=gpu)  # noqa: E731
+
+    def f(nm, inp):
+        return O.littlebit_forward(inp, H[nm], inp.shape[-1], P[nm].out_features, bias=B[nm])
+
+    def oracle(x, d0):
+        ya = f("a", x)
+        yb = f("b", ya)
+        yc = f("c", O.rms_norm(yb, w_c, EPS))
+        yd = f("d", yc)
+        hg = O.rms_norm(yd, w_g, EPS)
+        yg, yu = f("g", hg), f("u", hg)
+        ye = d0 + f("e", O.silu_mul(yg, yu))   # e adds into its residual buffer
+        yf = f("f", ye)
+        yh = f("h", O.rms_norm(yf, w_h, EPS))
+        return [ya, yb, yc, yd, yg, yu, ye, yf, yh]
+
+    def buffers():
+        return [nan(640), nan(512), nan(768), nan(384), nan(1000), nan(1000), nan(384), nan(512), nan(256)]
+
+    def links(o):
+        ya, yb, yc, yd, yg, yu, ye, yf, yh = o
+        return [ChainLink(P["a"], [ya]), ChainLink(P["b"], [yb]),
+                ChainLink(P["c"], [yc], rms_weight=tw_c, rms_eps=EPS), ChainLink(P["d"], [yd]),
+                ChainLink(LittleBitProjectionGroup([P["g"], P["u"]]), [yg, yu], rms_weight=tw_g, rms_eps=EPS),
+                ChainLink(P["e"], [ye], residuals=[ye], silu_mul=True), ChainLink(P["f"], [yf]),
+                ChainLink(P["h"], [yh], rms_weight=tw_h, rms_eps=EPS)]
+
+    import littlebit_amd._lib as L
+    assert L.LBK_MAX_CHAIN == 8
+    out = buffers()
+    chain = LittleBitChain(links(out))
+    for call in range(2):
+        x = rng.standard_normal((1, 512)).astype(np.float32)
+        d0 = rng.standard_normal((1, 384)).astype(np.float32)
+        tx = t(x)
+        assert chain.fused(tx)
+        out[6].copy_(t(d0))
+        chain.forward(tx)
+        # one by one
+        s = buffers()
+        P["a"].forward(tx, out=s[0])
+        P["b"].forward(s[0], out=s[1])
+        P["c"].forward(s[1], out=s[2], rms_weight=tw_c, rms_eps=EPS)
+        P["d"].forward(s[2], out=s[3])
+        LittleBitProjectionGroup([P["g"], P["u"]]).forward(s[3], outs=[s[4], s[5]], rms_weight=tw_g, rms_eps=EPS)
+        s[6].copy_(t(d0))
+        P["e"].forward(s[4], out=s[6], residual=s[6], x_up=s[5])
+        P["f"].forward(s[6], out=s[7])
+        P["h"].forward(s[7], out=s[8], rms_weight=tw_h, rms_eps=EPS)
+        torch.cuda.synchronize()
+        want = oracle(x.astype(np.float64), d0.astype(np.float64))
+        for i, (got, one, w) in enumerate(zip(out, s, want)):
+            y = got.cpu().numpy()
+            assert np.isfinite(y).all(), (call, i)
+            err, same = O.rel_err(y, w), O.rel_err(y, one.cpu().numpy())
+            print(f"[chain8] call {call} link output {i}: vs oracle {err:.2e}, vs one by one {same:.2e}", flush=True)
+            assert err <= TOL_F32, (call, i, err)
+            assert same <= 5e-5, (call, i, same)
