@@ -53,7 +53,7 @@ MEASURED_TRAFFIC = {"qkv": 1_229_984, "o": 616_288, "gate/up": 1_811_040, "down"
 MEASURED_TRAFFIC_M8 = {"qkv": 11_636_122, "o": 5_105_971, "gate/up": 17_666_765, "down": 9_626_419}
 # the same for one layer's chain (latent_mfma_kernel + 3 chain_mfma_kernel +
 # expand_mfma_kernel) of the chained draft step (profiles/littlebit_decode_chain.md)
-MEASURED_TRAFFIC_CHAIN = 4_729_994
+MEASURED_TRAFFIC_CHAIN = 4_604_313
 MALL_BYTES = 256 << 20
 
 
