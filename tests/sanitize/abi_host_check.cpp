@@ -198,6 +198,102 @@ int main() {
   EXPECT(lbk_lm_head_q4_argmax(static_cast<const uint8_t*>(ws), static_cast<const uint16_t*>(ws), 32000, 4100, xf,
                                nullptr, 1e-6f, nullptr, static_cast<int64_t*>(ws), ws, 1 << 20, nullptr) == LBK_ERR_ARG,
          "lm head hidden % 32");
+
+  // ---- chains (lbk_chain_*): a draft decoder layer o -> gate/up -> down ->
+  // next q/k/v, its planning and every error returned before a launch
+  {
+    auto tiled = [](int64_t rank, uintptr_t tag) {
+      lbk_branch b = branch(rank, tag);
+      b.v_sign_tiled = static_cast<const int32_t*>(fake(tag + 6));
+      return b;
+    };
+    lbk_branch bo = tiled(205, 100), bg = tiled(298, 110), bu = tiled(298, 120), bd = tiled(298, 130);
+    lbk_branch bq = tiled(205, 140), bk = tiled(205, 150), bv = tiled(205, 160);
+    void* X = const_cast<void*>(fake(200));
+    void* G = const_cast<void*>(fake(210));
+    void* U = const_cast<void*>(fake(220));
+    void* Q = const_cast<void*>(fake(230));
+    void* Kk = const_cast<void*>(fake(240));
+    void* V = const_cast<void*>(fake(250));
+    const float* Xr = static_cast<const float*>(X);
+    lbk_projection po{&bo, 1, 4096, nullptr, X, Xr};
+    lbk_projection pgu[2] = {{&bg, 1, 11008, nullptr, G, nullptr}, {&bu, 1, 11008, nullptr, U, nullptr}};
+    lbk_projection pdn{&bd, 1, 4096, nullptr, X, Xr};
+    lbk_projection pqkv[3] = {{&bq, 1, 4096, nullptr, Q, nullptr}, {&bk, 1, 4096, nullptr, Kk, nullptr},
+                              {&bv, 1, 4096, nullptr, V, nullptr}};
+    lbk_input plain{};
+    plain.kind = LBK_INPUT_PLAIN;
+    lbk_input rms2{}, rms1{}, silu{};
+    rms2.kind = rms1.kind = LBK_INPUT_RMSNORM;
+    rms2.rms_weight = static_cast<const float*>(fake(400));
+    rms1.rms_weight = static_cast<const float*>(fake(410));
+    rms2.rms_eps = rms1.rms_eps = 1e-5f;
+    silu.kind = LBK_INPUT_SILU_MUL;
+    lbk_chain_link layer[4] = {{&po, 1, 4096, &plain}, {pgu, 2, 4096, &rms2}, {&pdn, 1, 11008, &silu},
+                               {pqkv, 3, 4096, &rms1}};
+    const void* x0 = fake(300);
+    const size_t cw = lbk_chain_workspace_bytes(layer, 4);
+    EXPECT(cw > 0, "chain workspace");
+    EXPECT(cw >= lbk_group_workspace_bytes(pgu, 2, 1, 4096), "chain workspace below a link's");
+    EXPECT(lbk_chain_fused(layer, 4, x0) == 1, "the draft layer's chain runs joined");
+    EXPECT(lbk_chain_fused(layer, 1, x0) == 0, "one link runs as a call");
+    {
+      lbk_input silu0 = silu;  // the first link's SiLU * up reads the caller's x and x1
+      silu0.x1 = fake(310);
+      lbk_chain_link tail[2] = {{&pdn, 1, 11008, &silu0}, layer[3]};
+      EXPECT(lbk_chain_fused(tail, 2, x0) == 1, "down -> q/k/v with SiLU * up of the caller's x, x1");
+      lbk_chain_link nox1[2] = {{&pdn, 1, 11008, &silu}, layer[3]};
+      EXPECT(lbk_chain_fused(nox1, 2, x0) == LBK_ERR_ARG, "first link's SiLU * up without x1");
+    }
+    lbk_set_deterministic(1);
+    EXPECT(lbk_chain_fused(layer, 4, x0) == 0, "deterministic mode runs the links apart");
+    lbk_set_deterministic(0);
+    // without V's tiled copy the links run apart
+    lbk_branch bd_plain = bd;
+    bd_plain.v_sign_tiled = nullptr;
+    lbk_projection pdn_plain{&bd_plain, 1, 4096, nullptr, X, Xr};
+    lbk_chain_link untiled[4] = {layer[0], layer[1], {&pdn_plain, 1, 11008, &silu}, layer[3]};
+    EXPECT(lbk_chain_fused(untiled, 4, x0) == 0, "an untiled V runs apart");
+    // the longest chain: plain links alternating 4096 -> 4096
+    {
+      lbk_chain_link eight[LBK_MAX_CHAIN];
+      for (int j = 0; j < LBK_MAX_CHAIN; ++j) eight[j] = {&po, 1, 4096, &plain};
+      EXPECT(lbk_chain_workspace_bytes(eight, LBK_MAX_CHAIN) > 0, "eight links");
+      EXPECT(lbk_chain_fused(eight, LBK_MAX_CHAIN, x0) == 1, "eight links run joined");
+      lbk_chain_link nine[LBK_MAX_CHAIN + 1];
+      for (int j = 0; j <= LBK_MAX_CHAIN; ++j) nine[j] = {&po, 1, 4096, &plain};
+      EXPECT(lbk_chain_forward(nine, LBK_MAX_CHAIN + 1, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "nine links");
+    }
+    EXPECT(lbk_chain_forward(nullptr, 2, x0, ws, cw, nullptr) == LBK_ERR_ARG, "NULL links");
+    EXPECT(lbk_chain_forward(layer, 0, x0, ws, cw, nullptr) == LBK_ERR_ARG, "no links");
+    EXPECT(lbk_chain_forward(layer, 4, x0, ws, cw - 1, nullptr) == LBK_ERR_WORKSPACE, "small chain workspace");
+    EXPECT(lbk_chain_forward(layer, 4, x0, nullptr, cw, nullptr) == LBK_ERR_WORKSPACE, "NULL chain workspace");
+    {
+      lbk_chain_link bad[2] = {{&po, 1, 4096, &plain}, {&pdn, 1, 11008, &silu}};  // SiLU * up after one projection
+      EXPECT(lbk_chain_forward(bad, 2, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "SiLU after one projection");
+      EXPECT(std::strstr(lbk_last_error(), "link 1") != nullptr, "error names the link");
+    }
+    {
+      lbk_chain_link bad[2] = {{pgu, 2, 4096, &rms2}, {&po, 1, 4096, &plain}};  // plain after two projections
+      EXPECT(lbk_chain_forward(bad, 2, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "plain after two projections");
+    }
+    {
+      lbk_chain_link bad[2] = {{&po, 1, 4096, &plain}, {&pdn, 1, 11008, &plain}};  // K 11008 after N 4096
+      EXPECT(lbk_chain_forward(bad, 2, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "in_features mismatch");
+    }
+    {
+      lbk_input merge{};
+      merge.kind = LBK_INPUT_ATTN_MERGE;
+      merge.head_dim = 128;
+      merge.max_seq = 512;
+      lbk_chain_link bad[2] = {{&po, 1, 4096, &plain}, {&po, 1, 4096, &merge}};  // a merge input mid-chain
+      EXPECT(lbk_chain_forward(bad, 2, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "attention merge mid-chain");
+    }
+    {
+      lbk_chain_link bad[1] = {{&po, 0, 4096, &plain}};
+      EXPECT(lbk_chain_forward(bad, 1, x0, ws, 1u << 30, nullptr) == LBK_ERR_ARG, "link without projections");
+    }
+  }
   std::printf("%s (%d failures)\n", failures ? "FAILED" : "ok", failures);
   return failures ? 1 : 0;
 }
