@@ -329,3 +329,60 @@ def test_chain_eight_links(gpu):
             print(f"[chain8] call {call} link output {i}: vs oracle {err:.2e}, vs one by one {same:.2e}", flush=True)
             assert err <= TOL_F32, (call, i, err)
             assert same <= 5e-5, (call, i, same)
+
+
+def test_chain_first_link_input_kinds(gpu):
+    """Chains whose first link reads RMSNorm(x) * w (gate/up -> down) or
+    SiLU(gate) * up of the caller's tensors (down -> q/k/v), against the
+    oracle and the same calls one by one."""
+    from littlebit_amd import ChainLink, LittleBitChain, LittleBitProjectionGroup
+    Ly = Layer(9700, gpu, 512, 1000, 256, [40, 90], [64])
+    rng = np.random.Generator(np.random.PCG64(9701))
+    x = rng.standard_normal((1, 512)).astype(np.float32)
+    gt = rng.standard_normal((1, 1000)).astype(np.float32)
+    ut = rng.standard_normal((1, 1000)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(gpu)  # noqa: E731
+    f = lambda n, inp: O.littlebit_forward(inp, Ly.h[n], inp.shape[-1], Ly.p[n].out_features,  # noqa: E731
+                                           bias=Ly.b[n])
+    gu = LittleBitProjectionGroup([Ly.p["gate"], Ly.p["up"]])
+    qkv = LittleBitProjectionGroup([Ly.p["q"], Ly.p["k"], Ly.p["v"]])
+    nan = lambda n: torch.full((1, n), float("nan"), device=gpu)  # noqa: E731
+
+    # RMSNorm first: gate/up of RMSNorm(x) * ln2, then down of SiLU(gate) * up
+    g, u, d = nan(1000), nan(1000), nan(512)
+    chain = LittleBitChain([ChainLink(gu, [g, u], rms_weight=Ly.tln2, rms_eps=EPS),
+                            ChainLink(Ly.p["down"], [d], silu_mul=True)])
+    tx = t(x)
+    assert chain.fused(tx)
+    chain.forward(tx)
+    g1, u1, d1 = nan(1000), nan(1000), nan(512)
+    gu.forward(tx, outs=[g1, u1], rms_weight=Ly.tln2, rms_eps=EPS)
+    Ly.p["down"].forward(g1, out=d1, x_up=u1)
+    torch.cuda.synchronize()
+    h = O.rms_norm(x.astype(np.float64), Ly.ln2, EPS)
+    wg, wu = f("gate", h), f("up", h)
+    wd = f("down", O.silu_mul(wg, wu))
+    for name, got, one, want in (("gate", g, g1, wg), ("up", u, u1, wu), ("down", d, d1, wd)):
+        y = got.cpu().numpy()
+        err, same = O.rel_err(y, want), O.rel_err(y, one.cpu().numpy())
+        print(f"[chain-first] rmsnorm {name}: vs oracle {err:.2e}, vs one by one {same:.2e}", flush=True)
+        assert np.isfinite(y).all() and err <= TOL_F32 and same <= 5e-5, (name, err, same)
+
+    # SiLU * up first: down of SiLU(gt) * ut, then q/k/v of RMSNorm(down) * ln1
+    d, q, k, v = nan(512), nan(512), nan(256), nan(256)
+    chain = LittleBitChain([ChainLink(Ly.p["down"], [d], silu_mul=True),
+                            ChainLink(qkv, [q, k, v], rms_weight=Ly.tln1, rms_eps=EPS)])
+    tg, tu = t(gt), t(ut)
+    chain.forward(tg, x_up=tu)
+    d1, q1, k1, v1 = nan(512), nan(512), nan(256), nan(256)
+    Ly.p["down"].forward(tg, out=d1, x_up=tu)
+    qkv.forward(d1, outs=[q1, k1, v1], rms_weight=Ly.tln1, rms_eps=EPS)
+    torch.cuda.synchronize()
+    wd = f("down", O.silu_mul(gt.astype(np.float64), ut.astype(np.float64)))
+    h = O.rms_norm(wd, Ly.ln1, EPS)
+    for name, got, one, want in (("down", d, d1, wd), ("q", q, q1, f("q", h)), ("k", k, k1, f("k", h)),
+                                 ("v", v, v1, f("v", h))):
+        y = got.cpu().numpy()
+        err, same = O.rel_err(y, want), O.rel_err(y, one.cpu().numpy())
+        print(f"[chain-first] silu {name}: vs oracle {err:.2e}, vs one by one {same:.2e}", flush=True)
+        assert np.isfinite(y).all() and err <= TOL_F32 and same <= 5e-5, (name, err, same)
