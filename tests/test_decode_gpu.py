@@ -140,6 +140,48 @@ def test_attention_decode_kernel(gpu, heads, kvh, hd, max_seq, pos, device_pos):
         assert torch.equal(kc[:, :at], K[:, :at])  # nothing else changed
 
 
+@pytest.mark.parametrize("hd,pos", [(128, 0), (128, 37), (64, 100)])
+def test_attention_decode_ignores_rows_past_the_length(gpu, hd, pos):
+    """Cache rows past the new position may hold anything (here NaN and
+    Inf): the kernel reads whole chunks before it knows the position, and
+    those rows must not reach the output or the partials' merge."""
+    import littlebit_amd._lib as L
+    lib = L.load()
+    heads, kvh, max_seq = 4, 2, 160
+    need = lib.lbk_attention_partial_bytes(heads, max_seq, hd)
+    part = torch.empty(need // 4 + 1, device=gpu)
+    g = torch.Generator(device="cpu").manual_seed(pos + hd)
+    kc = torch.randn((kvh, max_seq, hd), generator=g)
+    vc = torch.randn((kvh, max_seq, hd), generator=g)
+    kc[:, pos + 1:] = float("nan")
+    vc[:, pos + 1::2] = float("inf")
+    vc[:, pos + 2::2] = float("nan")
+    q = torch.randn((heads * hd,), generator=g)
+    k = torch.randn((kvh * hd,), generator=g)
+    v = torch.randn((kvh * hd,), generator=g)
+    scale = hd ** -0.5
+    K, V = kc[:, :pos + 1].clone().double(), vc[:, :pos + 1].clone().double()
+    K[:, pos] = k.view(kvh, hd).double()
+    V[:, pos] = v.view(kvh, hd).double()
+    qg = q.view(kvh, heads // kvh, hd).double()
+    ref = torch.matmul(torch.softmax(torch.matmul(qg, K.transpose(1, 2).contiguous()) * scale, dim=-1), V).reshape(-1)
+    kc, vc, q, k, v = (t.to(gpu) for t in (kc, vc, q, k, v))
+    for out in (torch.full((heads * hd,), float("nan"), device=gpu), None):
+        rc = lib.lbk_attention_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), heads,
+                                      kvh, hd, max_seq, None, pos, scale, part.data_ptr(), part.numel() * 4,
+                                      None if out is None else out.data_ptr(), None)
+        L.check(rc, "lbk_attention_decode")
+        torch.cuda.synchronize()
+        if out is not None:
+            got = out.cpu().double()
+        else:  # the partials, merged on the host (chunks 0 .. pos // 16)
+            P = part[: heads * (-(-max_seq // 16)) * (hd + 4)].view(heads, -1, hd + 4)[:, : pos // 16 + 1].cpu().double()
+            w = torch.exp(P[..., hd] - P[..., hd].max(dim=1, keepdim=True).values)
+            got = ((w[..., None] * P[..., :hd]).sum(1) / (w * P[..., hd + 1]).sum(1)[:, None]).reshape(-1)
+        assert torch.isfinite(got).all()
+        assert O.rel_err(got.numpy(), ref.numpy()) <= 1e-5
+
+
 def test_attention_decode_rejects_bad_args(gpu):
     import littlebit_amd._lib as L
     lib = L.load()
