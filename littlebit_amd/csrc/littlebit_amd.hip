@@ -1964,7 +1964,6 @@ __global__ __launch_bounds__(W * kWave) void chain_mfma_kernel(ChainParams cp) {
 constexpr int kGB = 128;             // block tile (m and columns)
 constexpr int kGK = 64;              // k per step (two sign words per column)
 constexpr int kGThreads = 256;
-constexpr int kGChunks = kGB * kGK / 8 / kGThreads;  // 16-byte A chunks per thread per step
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -2121,7 +2120,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_scale_kernel(GemmParams p) {
 // (masked to zero past the row or the matrix) -- and a barrier makes the
 // tile, and the words step ks - 1 wrote, visible; fill(ks + 3) then refills
 // the stage and the register that step ks - 1 used.  Ends with a barrier.
-constexpr int kGStages = 4;
+[[maybe_unused]] constexpr int kGStages = 4;  // the ring's stages (one __shared__ array each)
 
 // Wave layout of a GEMM block: kGWM waves along m, kGWN along the columns;
 // a wave holds kGMI x NJ tiles of 32 x 32 (NJ = BN / (32 kGWN)).  The B
